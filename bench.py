@@ -1,0 +1,240 @@
+"""Benchmark of the Veda block-sparse attention hot path on one MI355X.
+
+Workload: one H3-scale layer, video grid 37x30x52 =
+57,720 tokens (seq_len 57,728), 48 heads, head_dim 128, bf16 q/k/v ~ N(0,1),
+tile shape (1,8,16) -> 592 query / key tiles, uniform random tile scores,
+equal-cost budget 0.1 * 451^2 / 592 with Bresenham rounding and the forced
+diagonal -> 20,340 kept 128x128 blocks per head (90% sparsity).
+
+A step = one block-sparse attention forward over all 48 heads with the block
+lists prebuilt (the reference bench's "kernel" timing,
+miowtion/kernels/bench.py:87-126). Reported beside it: "+prep" (selection,
+block mask and lists rebuilt per call), the full Veda layer (gather + pool of
+q / k / v, predictor, selection, lists, sparse forward, scatter), the dense
+baselines at the same shape, the roofline of the sparse kernel and the CPU
+baseline (the oracle's masked-dense attention + predictor on host cores).
+
+Prints ONE JSON line. Effective TFLOP/s counts computed blocks only,
+4 * 128 * 128 * D per kept block (miowtion/kernels/bench.py:52-60).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+import torch
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = 'block-sparse attn ms/layer + effective TFLOP/s @57.7k tok, 90% sparse, 1 GPU'
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+GRID = (37, 30, 52)
+HEADS = 48
+D = 128
+RATIO = 0.1
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _events_ms(fn, reps: int) -> list[float]:
+    """Per-call durations (ms) measured with events on the current stream,
+    which is the stream every op of this package launches on."""
+    out = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        b.synchronize()
+        out.append(a.elapsed_time(b))
+    return out
+
+
+def build_case(seed: int = 0):
+    from miowtion_amd import kernels, mask as pm, tiling as pt
+    used = GRID[0] * GRID[1] * GRID[2]
+    seq_len = -(-used // 64) * 64
+    lay = pt.build_tile_layout([pt.TiledSpan(0, GRID, pt.TileShape(1, 8, 16))], used, seq_len, 'cuda')
+    g = torch.Generator(device='cuda').manual_seed(seed)
+    q, k, v = (torch.randn(seq_len, HEADS, D, generator=g, device='cuda').to(torch.bfloat16)
+               for _ in range(3))
+    for t in (q, k, v):
+        t[used:] = 0
+    scores = torch.rand(HEADS, lay.n_tiles, lay.n_tiles, generator=g, device='cuda')
+    qt, kt, vt = (kernels.gather_tiles(t, lay, None) for t in (q, k, v))
+    blocks = pm.column_blocks(lay, pm.Budget(ratio=RATIO))
+
+    def prep():
+        sel = pm.select_video_blocks(scores, lay, blocks)
+        mask = pm.dense_block_mask(sel, lay)
+        return mask, kernels.index_lists(mask, lay)
+
+    mask, lists = prep()
+    return dict(lay=lay, q=q, k=k, v=v, qt=qt, kt=kt, vt=vt, scores=scores, prep=prep,
+                mask=mask, lists=lists, used=used, seq_len=seq_len)
+
+
+def cpu_baseline(budget_s: float = 20.0) -> dict:
+    """The oracle (the reference's CPU torch path restated: predictor pooling +
+    logits + top-k, and masked-dense fp32 attention) on host cores, on a
+    bounded sample of the C2 workload: 1 head, query tiles taken in order until
+    the time budget is spent; scaled to all 592 x 48 query tiles."""
+    from oracle import attention as oa, mask as om, predictor as op, tiling as ot
+    used = GRID[0] * GRID[1] * GRID[2]
+    seq_len = -(-used // 64) * 64
+    lay = ot.build_layout([ot.Span(0, GRID, ot.Shape(1, 8, 16))], used, seq_len)
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(seq_len, 1, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    qt, kt, vt = (ot.gather_tiles(t, lay, None) for t in (q, k, v))
+    t0 = time.perf_counter()
+    pq = torch.randn(1, 3 * D, D, generator=g) * 0.02
+    pk = torch.randn(1, 3 * D, D, generator=g) * 0.02
+    logits = op.logits(op.pool_tiles(qt, lay), op.pool_tiles(kt, lay), pq, pk, torch.tensor([0]))
+    idx, keep = om.select_video_blocks(logits, lay, om.column_blocks(lay, om.Budget(ratio=RATIO)))
+    mask = om.dense_block_mask(idx, keep, lay)
+    t_pred = time.perf_counter() - t0
+    n = lay.n_tiles
+    done, t_attn, blocks = 0, 0.0, 0
+    step = 4
+    while done < n and t_attn < budget_s:
+        rows = torch.arange(done, min(done + step, n))
+        sub_q = qt.view(n, 128, 1, D)[rows].reshape(-1, 1, D)
+        t1 = time.perf_counter()
+        oa.block_sparse_attention(sub_q, kt, vt, mask[:, rows], lay.valid_count, q_chunk=512)
+        t_attn += time.perf_counter() - t1
+        blocks += int(mask[:, rows].sum())
+        done += rows.numel()
+    per_tile = t_attn / done
+    layer_s = (per_tile * n + t_pred) * HEADS
+    flop = 4.0 * 128 * 128 * D * 20340 * HEADS
+    return {'value': round(flop / layer_s / 1e12, 6), 'unit': 'TFLOP/s (effective)',
+            'ms_per_layer': round(layer_s * 1e3, 1),
+            'cores': torch.get_num_threads(), 'os_cpu_count': os.cpu_count(), 'kind': 'port',
+            'sample': (f'C2, 1 of {HEADS} heads: predictor (pool + logits + top-k) on all '
+                       f'{n} tiles and masked-dense fp32 attention on {done} of {n} query tiles '
+                       f'({t_attn:.1f} s); scaled linearly to {n} tiles x {HEADS} heads')}
+
+
+def _traffic() -> float | None:
+    f = ROOT / 'profiles' / 'sparse_fwd_c2_traffic.json'
+    if f.exists():
+        try:
+            return json.loads(f.read_text()).get('hbm_bytes_per_launch')
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=20)
+    ap.add_argument('--warmup', type=int, default=3)
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-dense', action='store_true')
+    ap.add_argument('--cpu-budget', type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU only (asked for --gpus {args.gpus}); the Veda path '
+              'shards by head with no exchange inside the layer, so N GPUs run N independent '
+              'shares -- run with --gpus 1', file=sys.stderr)
+        return 2
+    from miowtion_amd import kernels, mask as pm
+    _log('bench: building C2 case')
+    c = build_case()
+    lay = c['lay']
+    kept = int(c['mask'].sum())
+    assert kept == 20340 * HEADS, kept
+    flop = 4.0 * 128 * 128 * D * kept
+    dense_flop = 4.0 * c['used'] * c['used'] * HEADS * D
+
+    def step():
+        return kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'], c['lists'], lay)
+
+    _log(f'bench: warmup {args.warmup}')
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _log(f'bench: timing {args.steps} steps')
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    kernel_ms = sorted(_events_ms(step, max(5, args.steps)))
+    k_ms = kernel_ms[len(kernel_ms) // 2]
+    k_avg = sum(kernel_ms) / len(kernel_ms)
+    achieved = flop / (k_avg * 1e-3) / 1e12
+
+    _log('bench: +prep and full layer')
+    prep_ms = sorted(_events_ms(lambda: c['prep'](), 5))[2]
+    from miowtion_amd import attention as pa, plan as pplan, predictor as pp, tiling as pt
+    layout = pa.PackedLayout((pa.VideoSpan(0, GRID),), c['used'], c['seq_len'])
+    clip = pa.ClipTiling(layout, pa.VedaConfig(target_budget=pm.Budget(ratio=RATIO)), 'cuda')
+    plan = pplan.TilePlan.uniform('16x9_t37_c2', GRID, pt.TileShape(1, 8, 16), 1, HEADS)
+    pred = pp.TileScorePredictor([pp.LayerPredictor.random(
+        HEADS, D, std=0.02, generator=torch.Generator().manual_seed(1), device='cuda', fp8=True)])
+    student = pa.SparseStudent(clip, plan, pred)
+    layer_ms = sorted(_events_ms(lambda: student(c['q'], c['k'], c['v'], 0), 5))[2]
+
+    dense = {}
+    if not args.no_dense:
+        _log('bench: dense baselines')
+        qd, kd, vd = (t[:c['used']].transpose(0, 1)[None] for t in (c['q'], c['k'], c['v']))
+        try:
+            sdpa = sorted(_events_ms(lambda: torch.nn.functional.scaled_dot_product_attention(
+                qd, kd, vd), 3))[1]
+            dense['torch_sdpa_ms'] = round(sdpa, 3)
+        except RuntimeError as e:  # a backend refusal is reported, not hidden
+            dense['torch_sdpa_error'] = str(e)[:200]
+        own = sorted(_events_ms(lambda: kernels.dense_attention(c['q'], c['k'], c['v'], c['used']), 3))[1]
+        dense['own_dense_ms'] = round(own, 3)
+        best = min(v for k_, v in dense.items() if k_.endswith('_ms'))
+        dense['speedup_vs_best_dense'] = round(best / k_ms, 2)
+        dense['efficiency'] = round(best * (kept / (HEADS * 592 * 592)) / k_ms, 3)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        _log('bench: cpu baseline')
+        cpu = cpu_baseline(args.cpu_budget)
+
+    line = {
+        'metric': METRIC,
+        'value': round(flop / (k_ms * 1e-3) / 1e12, 2),
+        'unit': 'TFLOP/s (effective, computed blocks)',
+        'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
+        'ms_per_step': round(k_ms, 4),
+        'ms_per_step_wall': round(wall_ms, 4),
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+        'dtype': 'bf16', 'data': 'synthetic (seeded N(0,1) q/k/v, uniform random tile scores)',
+        'config': {'workload': 'BASELINE C2: 57,720 tok (37x30x52) x 48 heads x d128, tiles '
+                               '(1,8,16) -> 592, keep 0.1 -> 20,340 blocks/head, forced diagonal, '
+                               'sparse forward with prebuilt lists',
+                   'kept_blocks': kept, 'flop_per_launch': flop,
+                   'dense_equivalent_flop': dense_flop},
+        'ms_per_layer': {'kernel': round(k_ms, 4), 'plus_prep': round(k_ms + prep_ms, 4),
+                         'prep': round(prep_ms, 4), 'full_veda_layer': round(layer_ms, 4)},
+        'dense_equivalent_tflops': round(dense_flop / (k_ms * 1e-3) / 1e12, 2),
+        'dense': dense,
+        'roofline': {'bound': 'mfma', 'achieved': round(achieved, 2), 'peak': PEAK_BF16_TFLOPS,
+                     'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_BF16_TFLOPS, 4),
+                     'traffic': _traffic(), 'kernel': 'fwd_kernel<false> (veda_block_sparse_fwd)',
+                     'avg_launch_ms': round(k_avg, 4)},
+        'cpu_baseline': cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == '__main__':
+    sys.exit(main())

@@ -1,0 +1,230 @@
+// Block selection: equal-budget top-k per query tile, the block mask, and
+// the full / partial key-tile lists the attention kernel walks.
+//
+// Top-k: one wave per (head, query tile). The score row lives in LDS as
+// 64-bit keys (orderable fp32 score << 32 | ~column), lane-strided so every
+// LDS access is conflict-free; each lane caches the best key of its own
+// columns and k_hi rounds of a wave-wide max extract the winners in
+// descending order. Folding the column into the key makes every key
+// distinct, so the order is total: higher score first, lower column first on
+// equal scores.
+//
+// Lists: one wave per (head, row), 64 columns per step, positions from a
+// ballot + popcount prefix (no sort, no atomics).
+
+#include "veda_common.h"
+
+namespace veda {
+namespace {
+
+__device__ __forceinline__ uint32_t orderable(float v) {
+  if (v == 0.f) v = 0.f;  // -0 ties with +0, as in a float comparison
+  uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+constexpr uint32_t kNegInfKey = 0x007fffffu;  // orderable(-inf)
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    uint32_t lo = __shfl_xor((uint32_t)v, m, 64);
+    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+    uint64_t o = ((uint64_t)hi << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+constexpr int kMaxCols = 2048;  // columns of one block (FA4's 2048-block cap)
+constexpr int kSelWaves = 4;
+
+__global__ void __launch_bounds__(256) select_topk_kernel(
+    const float* __restrict__ scores, int64_t n_heads, int64_t n_rows, int64_t ssh,
+    int64_t ssr, int64_t block_start, int n_cols, const uint8_t* __restrict__ kv_ok,
+    const int64_t* __restrict__ rows, int k_lo, int k_hi, const uint8_t* __restrict__ extra,
+    int64_t n_extra, int64_t* __restrict__ index, uint8_t* __restrict__ keep, int64_t osh,
+    int64_t osr, int64_t col0) {
+  __shared__ uint64_t keys[kSelWaves][kMaxCols];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * kSelWaves + wave;
+  if (item >= n_heads * n_rows) return;  // whole wave exits together
+  const int64_t h = item / n_rows, r = item % n_rows;
+  const int64_t tile_id = rows[r];
+  const int64_t diag = tile_id - block_start;  // column of the own tile, if in block
+  const float* srow = scores + h * ssh + r * ssr + block_start;
+  uint64_t* kv = keys[wave];
+  const int per_lane = (n_cols + 63) / 64;
+  uint64_t best = 0;
+  int best_j = 0;
+  for (int j = 0; j < per_lane; ++j) {
+    const int c = j * 64 + lane;
+    uint64_t key = 0;  // absent column: below every real key
+    if (c < n_cols) {
+      float v = srow[c];
+      if (!kv_ok[block_start + c]) v = -INFINITY;
+      if (c == diag) v = INFINITY;
+      key = ((uint64_t)orderable(v) << 32) | (uint32_t)(~(uint32_t)c);
+    }
+    kv[j * 64 + lane] = key;
+    if (key > best) {
+      best = key;
+      best_j = j;
+    }
+  }
+  const bool has_extra = tile_id >= 0 && tile_id < n_extra && extra[tile_id] != 0;
+  const int allowed = k_lo + (has_extra ? 1 : 0);
+  int64_t* irow = index + h * osh + r * osr + col0;
+  uint8_t* krow = keep + h * osh + r * osr + col0;
+  for (int t = 0; t < k_hi; ++t) {
+    const uint64_t top = wave_max_u64(best);
+    const uint32_t c = ~(uint32_t)top;
+    const uint32_t vkey = (uint32_t)(top >> 32);
+    if ((int)(c & 63) == lane) {
+      irow[t] = block_start + (int64_t)c;
+      krow[t] = (t < allowed && vkey > kNegInfKey) ? 1 : 0;
+      kv[best_j * 64 + lane] = 0;
+      best = 0;
+      best_j = 0;
+      for (int j = 0; j < per_lane; ++j) {
+        const uint64_t key = kv[j * 64 + lane];
+        if (key > best) {
+          best = key;
+          best_j = j;
+        }
+      }
+    }
+  }
+}
+
+constexpr int kMaxTiles = 8192;
+
+__global__ void __launch_bounds__(256) dense_mask_kernel(
+    const int64_t* __restrict__ index, const uint8_t* __restrict__ keep, int64_t n_sel,
+    int64_t k_total, const uint8_t* __restrict__ kv_ok, int n_tiles, int64_t n_video,
+    int64_t out_rows, uint8_t* __restrict__ mask) {
+  __shared__ uint8_t row[kMaxTiles];
+  const int64_t h = blockIdx.x / out_rows, r = blockIdx.x % out_rows;
+  const bool video_row = r < n_sel && r < n_video;
+  for (int c = threadIdx.x; c < n_tiles; c += blockDim.x)
+    row[c] = (!video_row || c >= n_video) ? kv_ok[c] : 0;
+  __syncthreads();
+  if (video_row) {
+    const int64_t base = (h * n_sel + r) * k_total;
+    for (int64_t t = threadIdx.x; t < k_total; t += blockDim.x) {
+      const int64_t c = index[base + t];
+      if (keep[base + t] && c >= 0 && c < n_tiles) row[c] = 1;
+    }
+  }
+  __syncthreads();
+  uint8_t* out = mask + (h * out_rows + r) * n_tiles;
+  for (int c = threadIdx.x; c < n_tiles; c += blockDim.x) out[c] = row[c];
+}
+
+__global__ void __launch_bounds__(256) index_lists_kernel(
+    const uint8_t* __restrict__ mask, int64_t n_items, int n_tiles,
+    const uint8_t* __restrict__ kv_ok, const uint8_t* __restrict__ full_tile,
+    int32_t* __restrict__ part_cnt, int32_t* __restrict__ part_idx,
+    int32_t* __restrict__ full_cnt, int32_t* __restrict__ full_idx) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
+  if (item >= n_items) return;
+  const uint8_t* m = mask + item * n_tiles;
+  int32_t* fi = full_idx + item * n_tiles;
+  int32_t* pi = part_idx + item * n_tiles;
+  const uint64_t below = (1ull << lane) - 1ull;
+  int nf = 0, np = 0;
+  for (int c0 = 0; c0 < n_tiles; c0 += 64) {
+    const int c = c0 + lane;
+    bool f = false, p = false;
+    if (c < n_tiles && m[c] && kv_ok[c]) {
+      f = full_tile[c] != 0;
+      p = !f;
+    }
+    const uint64_t bf = __ballot(f), bp = __ballot(p);
+    if (f) fi[nf + __popcll(bf & below)] = c;
+    if (p) pi[np + __popcll(bp & below)] = c;
+    nf += __popcll(bf);
+    np += __popcll(bp);
+  }
+  // Non-members follow, ascending (the stable argsort of ~member).
+  int of = nf, op = np;
+  for (int c0 = 0; c0 < n_tiles; c0 += 64) {
+    const int c = c0 + lane;
+    bool f = false, p = false;
+    if (c < n_tiles) {
+      const bool member = m[c] && kv_ok[c];
+      const bool full = full_tile[c] != 0;
+      f = !(member && full);
+      p = !(member && !full);
+    }
+    const uint64_t bf = __ballot(f), bp = __ballot(p);
+    if (f) fi[of + __popcll(bf & below)] = c;
+    if (p) pi[op + __popcll(bp & below)] = c;
+    of += __popcll(bf);
+    op += __popcll(bp);
+  }
+  if (lane == 0) {
+    full_cnt[item] = nf;
+    part_cnt[item] = np;
+  }
+}
+
+}  // namespace
+}  // namespace veda
+
+using namespace veda;
+
+extern "C" int veda_select_topk(const float* scores, int64_t n_heads, int64_t n_rows,
+                                int64_t s_stride_h, int64_t s_stride_r, int64_t block_start,
+                                int64_t n_cols, const uint8_t* kv_ok, const int64_t* rows,
+                                int64_t k_lo, int64_t k_hi, const uint8_t* extra,
+                                int64_t n_extra, int64_t* index, uint8_t* keep,
+                                int64_t o_stride_h, int64_t o_stride_r, int64_t col0,
+                                void* stream) {
+  VEDA_REQUIRE(n_cols >= 1 && n_cols <= kMaxCols, "select_topk: n_cols %lld not in [1, %d]",
+               (long long)n_cols, kMaxCols);
+  VEDA_REQUIRE(1 <= k_lo && k_lo <= k_hi && k_hi <= n_cols,
+               "select_topk: need 1 <= k_lo <= k_hi <= n_cols, got %lld %lld %lld",
+               (long long)k_lo, (long long)k_hi, (long long)n_cols);
+  VEDA_REQUIRE(block_start >= 0 && n_heads >= 0 && n_rows >= 0, "select_topk: negative size");
+  const int64_t items = n_heads * n_rows;
+  if (items == 0) return VEDA_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  select_topk_kernel<<<(unsigned)((items + kSelWaves - 1) / kSelWaves), 256, 0, s>>>(
+      scores, n_heads, n_rows, s_stride_h, s_stride_r, block_start, (int)n_cols, kv_ok, rows,
+      (int)k_lo, (int)k_hi, extra, n_extra, index, keep, o_stride_h, o_stride_r, col0);
+  return check_launch("veda_select_topk");
+}
+
+extern "C" int veda_dense_block_mask(const int64_t* index, const uint8_t* keep, int64_t n_heads,
+                                     int64_t n_sel, int64_t k_total, const uint8_t* kv_ok,
+                                     int64_t n_tiles, int64_t n_video, int global_rows,
+                                     uint8_t* mask, void* stream) {
+  VEDA_REQUIRE(n_tiles >= 1 && n_tiles <= kMaxTiles, "dense_block_mask: n_tiles %lld > %d",
+               (long long)n_tiles, kMaxTiles);
+  VEDA_REQUIRE(!global_rows || n_sel == n_video,
+               "dense_block_mask: global_rows needs a selection of all video rows");
+  const int64_t out_rows = global_rows ? n_tiles : n_sel;
+  const int64_t blocks = n_heads * out_rows;
+  if (blocks == 0) return VEDA_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dense_mask_kernel<<<(unsigned)blocks, 256, 0, s>>>(index, keep, n_sel, k_total, kv_ok,
+                                                     (int)n_tiles, n_video, out_rows, mask);
+  return check_launch("veda_dense_block_mask");
+}
+
+extern "C" int veda_index_lists(const uint8_t* block_mask, int64_t n_heads, int64_t n_rows,
+                                int64_t n_tiles, const uint8_t* kv_ok, const uint8_t* full_tile,
+                                int32_t* part_cnt, int32_t* part_idx, int32_t* full_cnt,
+                                int32_t* full_idx, void* stream) {
+  VEDA_REQUIRE(n_tiles >= 1 && n_tiles < (1ll << 31), "index_lists: bad n_tiles");
+  const int64_t items = n_heads * n_rows;
+  if (items == 0) return VEDA_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  index_lists_kernel<<<(unsigned)((items + 3) / 4), 256, 0, s>>>(
+      block_mask, items, (int)n_tiles, kv_ok, full_tile, part_cnt, part_idx, full_cnt, full_idx);
+  return check_launch("veda_index_lists");
+}

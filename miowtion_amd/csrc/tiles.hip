@@ -1,0 +1,349 @@
+// Tile permutation kernels: gather (+ pooling, + second moments), scatter
+// and the LSE gather. All three are HBM-bound copies.
+//
+// Work split: one 256-thread workgroup per (tile, group of heads). A wave
+// owns 32 of the tile's 128 slots; inside the wave, lane = (head, 16-byte
+// chunk of head_dim), so every load and store of a slot's row moves
+// `heads_per_group * head_dim * 2` contiguous bytes (heads are adjacent in
+// the [S, H, D] input and in the [N, H', D] output). Pooling statistics are
+// reduced in registers over the wave's 32 slots and across the 4 waves
+// through LDS, so the tile is read from HBM exactly once (the centred
+// variance, when asked for, re-reads it from L2).
+
+#include "veda_common.h"
+
+#include <cstring>
+#include <string>
+
+namespace veda {
+
+namespace {
+thread_local std::string g_error;
+}
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+}
+
+int check_launch(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(err));
+    return VEDA_ELAUNCH;
+  }
+  return VEDA_OK;
+}
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kSlotsPerWave = kTile / kWaves;  // 32
+
+struct Row8 {
+  uint32_t w[4];  // 8 bf16 values
+};
+
+__device__ __forceinline__ Row8 load_row8(const uint16_t* p) {
+  u32x4 v = *reinterpret_cast<const u32x4*>(p);
+  return Row8{{v[0], v[1], v[2], v[3]}};
+}
+
+__device__ __forceinline__ void store_row8(uint16_t* p, const Row8& r) {
+  u32x4 v = {r.w[0], r.w[1], r.w[2], r.w[3]};
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+
+__device__ __forceinline__ float elem(const Row8& r, int e) {
+  uint32_t w = r.w[e >> 1];
+  return bf16_to_f32((e & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+template <int D, bool POOL, bool SECOND>
+__global__ void __launch_bounds__(256) gather_kernel(
+    const uint16_t* __restrict__ x, int64_t x_rows, int64_t x_heads,
+    int64_t xs, int64_t xh, const int64_t* __restrict__ gather_index,
+    const int32_t* __restrict__ slot_valid,
+    const int32_t* __restrict__ valid_count, int64_t n_tiles,
+    const int64_t* __restrict__ heads, int64_t n_heads,
+    uint16_t* __restrict__ out, int64_t os, int64_t oh,
+    float* __restrict__ feats, float* __restrict__ sq, float* __restrict__ var) {
+  constexpr int kChunks = D / 8;          // 16-byte chunks per head row
+  constexpr int kHeadsPerGroup = 64 / kChunks;
+  const int tile = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int hl = lane / kChunks;
+  const int chunk = lane % kChunks;
+  const int64_t hp = (int64_t)blockIdx.y * kHeadsPerGroup + hl;  // h'
+  const bool head_ok = hp < n_heads;
+  const int64_t head = head_ok ? heads[hp] : 0;
+  const bool src_head_ok = head_ok && head >= 0 && head < x_heads;
+  const int64_t slot0 = (int64_t)tile * kTile + wave * kSlotsPerWave;
+  const int count = POOL ? valid_count[tile] : 0;
+
+  float s_sum[8], s_max[8], s_min[8], s_sq[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    s_sum[e] = 0.f;
+    s_max[e] = -INFINITY;
+    s_min[e] = INFINITY;
+    s_sq[e] = 0.f;
+  }
+
+#pragma unroll 8
+  for (int i = 0; i < kSlotsPerWave; ++i) {
+    const int64_t slot = slot0 + i;
+    const int64_t src = gather_index[slot];
+    const bool ok = slot_valid[slot] != 0 && src_head_ok && src >= 0 && src < x_rows;
+    Row8 r = {{0u, 0u, 0u, 0u}};
+    if (ok) r = load_row8(x + src * xs + head * xh + chunk * 8);
+    if (head_ok && out != nullptr) store_row8(out + slot * os + hp * oh + chunk * 8, r);
+    if (POOL) {
+      const bool real = (wave * kSlotsPerWave + i) < count;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = elem(r, e);
+        s_sum[e] += f;
+        if (real) {
+          s_max[e] = fmaxf(s_max[e], f);
+          s_min[e] = fminf(s_min[e], f);
+        }
+        if (SECOND) s_sq[e] += f * f;
+      }
+    }
+  }
+  if (!POOL) return;
+
+  // Cross-wave reduction through LDS: [stat][wave][lane][8].
+  constexpr int kStats = SECOND ? 4 : 3;
+  __shared__ float red[kStats][kWaves][64][8];
+  __shared__ float mean_lds[64][8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    red[0][wave][lane][e] = s_sum[e];
+    red[1][wave][lane][e] = s_max[e];
+    red[2][wave][lane][e] = s_min[e];
+    if (SECOND) red[kStats - 1][wave][lane][e] = s_sq[e];
+  }
+  __syncthreads();
+  const bool empty = count == 0;
+  const float denom = (float)(count > 1 ? count : 1);
+  const int64_t fbase = (hp * n_tiles + tile);
+  if (wave == 0) {
+    float mean[8], mx[8], mn[8], sqv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float a = red[0][0][lane][e], b = red[1][0][lane][e], c = red[2][0][lane][e];
+      float d = SECOND ? red[kStats - 1][0][lane][e] : 0.f;
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) {
+        a += red[0][w][lane][e];
+        b = fmaxf(b, red[1][w][lane][e]);
+        c = fminf(c, red[2][w][lane][e]);
+        if (SECOND) d += red[kStats - 1][w][lane][e];
+      }
+      mean[e] = a / denom;
+      mean_lds[lane][e] = mean[e];
+      mx[e] = empty ? 0.f : b;
+      mn[e] = empty ? 0.f : c;
+      sqv[e] = empty ? 0.f : d / denom;
+      if (empty) mean[e] = 0.f;
+    }
+    if (head_ok) {
+      float* f = feats + fbase * (3 * D) + chunk * 8;
+#pragma unroll
+      for (int e = 0; e < 8; e += 4) {
+        *reinterpret_cast<f32x4*>(f + e) = f32x4{mean[e], mean[e + 1], mean[e + 2], mean[e + 3]};
+        *reinterpret_cast<f32x4*>(f + D + e) = f32x4{mx[e], mx[e + 1], mx[e + 2], mx[e + 3]};
+        *reinterpret_cast<f32x4*>(f + 2 * D + e) = f32x4{mn[e], mn[e + 1], mn[e + 2], mn[e + 3]};
+        if (SECOND)
+          *reinterpret_cast<f32x4*>(sq + fbase * D + chunk * 8 + e) =
+              f32x4{sqv[e], sqv[e + 1], sqv[e + 2], sqv[e + 3]};
+      }
+    }
+  }
+  if (!SECOND) return;
+  __syncthreads();
+  // Second pass for the centred variance (predictor.py:133-168 computes it
+  // two-pass on purpose): sum over real rows of (x - mean)^2.
+  float mean[8], acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    mean[e] = mean_lds[lane][e];
+    acc[e] = 0.f;
+  }
+#pragma unroll 8
+  for (int i = 0; i < kSlotsPerWave; ++i) {
+    const int64_t slot = slot0 + i;
+    if (wave * kSlotsPerWave + i >= count) break;
+    const int64_t src = gather_index[slot];
+    const bool ok = slot_valid[slot] != 0 && src_head_ok && src >= 0 && src < x_rows;
+    Row8 r = {{0u, 0u, 0u, 0u}};
+    if (ok) r = load_row8(x + src * xs + head * xh + chunk * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float c = elem(r, e) - mean[e];
+      acc[e] += c * c;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[0][wave][lane][e] = acc[e];
+  __syncthreads();
+  if (wave == 0 && head_ok) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float a = red[0][0][lane][e];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) a += red[0][w][lane][e];
+      v[e] = empty ? 0.f : a / denom;
+    }
+    float* o = var + fbase * D + chunk * 8;
+    *reinterpret_cast<f32x4*>(o) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(o + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  }
+}
+
+template <int D>
+__global__ void __launch_bounds__(256) scatter_kernel(
+    const uint16_t* __restrict__ tiled, int64_t ts, int64_t th,
+    const int64_t* __restrict__ scatter_index,
+    const int32_t* __restrict__ slot_valid, const int64_t* __restrict__ heads,
+    int64_t n_heads, uint16_t* __restrict__ out, int64_t out_rows,
+    int64_t out_heads, int64_t os, int64_t oh) {
+  constexpr int kChunks = D / 8;
+  constexpr int kHeadsPerGroup = 64 / kChunks;
+  const int tile = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t hp = (int64_t)blockIdx.y * kHeadsPerGroup + lane / kChunks;
+  const int chunk = lane % kChunks;
+  if (hp >= n_heads) return;
+  const int64_t head = heads[hp];
+  if (head < 0 || head >= out_heads) return;
+  const int64_t slot0 = (int64_t)tile * kTile + wave * kSlotsPerWave;
+#pragma unroll 8
+  for (int i = 0; i < kSlotsPerWave; ++i) {
+    const int64_t slot = slot0 + i;
+    const int64_t dst = scatter_index[slot];
+    if (slot_valid[slot] == 0 || dst < 0 || dst >= out_rows) continue;
+    Row8 r = load_row8(tiled + slot * ts + hp * th + chunk * 8);
+    store_row8(out + dst * os + head * oh + chunk * 8, r);
+  }
+}
+
+__global__ void gather_lse_kernel(const float* __restrict__ lse, int64_t rows,
+                                  int64_t n_src_heads, int64_t ls, int64_t lh,
+                                  const int64_t* __restrict__ gather_index,
+                                  const int32_t* __restrict__ slot_valid,
+                                  int64_t n_slots, const int64_t* __restrict__ heads,
+                                  int64_t n_heads, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_slots * n_heads) return;
+  const int64_t s = i / n_heads, hp = i % n_heads;
+  const int64_t src = gather_index[s];
+  const int64_t head = heads[hp];
+  float v = 0.f;
+  if (slot_valid[s] != 0 && src >= 0 && src < rows && head >= 0 && head < n_src_heads)
+    v = lse[src * ls + head * lh];
+  out[i] = v;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace veda
+
+using namespace veda;
+
+extern "C" const char* veda_last_error(void) { return g_error.c_str(); }
+
+extern "C" int veda_abi_version(void) { return 1; }
+
+extern "C" int veda_gather_tiles(const void* x, int64_t x_rows, int64_t x_heads,
+                                 int64_t x_stride_s, int64_t x_stride_h,
+                                 const int64_t* gather_index, const int32_t* slot_valid,
+                                 const int32_t* valid_count, int64_t n_tiles,
+                                 const int64_t* heads, int64_t n_heads, int64_t head_dim,
+                                 void* out, int64_t out_stride_s, int64_t out_stride_h,
+                                 float* feats, float* sq, float* var, void* stream) {
+  VEDA_REQUIRE(head_dim == 64 || head_dim == 128, "gather: head_dim must be 64 or 128, got %lld",
+               (long long)head_dim);
+  VEDA_REQUIRE(n_tiles >= 0 && n_heads >= 0, "gather: negative size");
+  VEDA_REQUIRE(x_stride_s % 8 == 0 && x_stride_h % 8 == 0 && out_stride_s % 8 == 0 &&
+                   out_stride_h % 8 == 0 && aligned16(x) && aligned16(out),
+               "gather: rows must be 16-byte aligned (strides multiple of 8 elements)");
+  VEDA_REQUIRE((sq == nullptr) == (var == nullptr), "gather: sq and var go together");
+  VEDA_REQUIRE(feats != nullptr || sq == nullptr, "gather: second moments need pooling");
+  VEDA_REQUIRE(feats == nullptr || valid_count != nullptr, "gather: pooling needs valid_count");
+  if (n_tiles == 0 || n_heads == 0) return VEDA_OK;
+  const int hpg = head_dim == 128 ? 4 : 8;
+  dim3 grid((unsigned)n_tiles, (unsigned)((n_heads + hpg - 1) / hpg));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  auto xx = static_cast<const uint16_t*>(x);
+  auto oo = static_cast<uint16_t*>(out);
+#define VEDA_GATHER(D, P, S2)                                                                  \
+  gather_kernel<D, P, S2><<<grid, 256, 0, s>>>(xx, x_rows, x_heads, x_stride_s, x_stride_h,   \
+                                               gather_index, slot_valid, valid_count, n_tiles, \
+                                               heads, n_heads, oo, out_stride_s, out_stride_h, \
+                                               feats, sq, var)
+  if (head_dim == 128) {
+    if (!feats) VEDA_GATHER(128, false, false);
+    else if (!sq) VEDA_GATHER(128, true, false);
+    else VEDA_GATHER(128, true, true);
+  } else {
+    if (!feats) VEDA_GATHER(64, false, false);
+    else if (!sq) VEDA_GATHER(64, true, false);
+    else VEDA_GATHER(64, true, true);
+  }
+#undef VEDA_GATHER
+  return check_launch("veda_gather_tiles");
+}
+
+extern "C" int veda_scatter_tiles(const void* tiled, int64_t tiled_stride_s,
+                                  int64_t tiled_stride_h, const int64_t* scatter_index,
+                                  const int32_t* slot_valid, int64_t n_tiles,
+                                  const int64_t* heads, int64_t n_heads, int64_t head_dim,
+                                  void* out, int64_t out_rows, int64_t out_heads,
+                                  int64_t out_stride_s, int64_t out_stride_h, void* stream) {
+  VEDA_REQUIRE(head_dim == 64 || head_dim == 128, "scatter: head_dim must be 64 or 128, got %lld",
+               (long long)head_dim);
+  VEDA_REQUIRE(tiled_stride_s % 8 == 0 && tiled_stride_h % 8 == 0 && out_stride_s % 8 == 0 &&
+                   out_stride_h % 8 == 0 && aligned16(tiled) && aligned16(out),
+               "scatter: rows must be 16-byte aligned (strides multiple of 8 elements)");
+  if (n_tiles == 0 || n_heads == 0) return VEDA_OK;
+  const int hpg = head_dim == 128 ? 4 : 8;
+  dim3 grid((unsigned)n_tiles, (unsigned)((n_heads + hpg - 1) / hpg));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  auto tt = static_cast<const uint16_t*>(tiled);
+  auto oo = static_cast<uint16_t*>(out);
+  if (head_dim == 128)
+    scatter_kernel<128><<<grid, 256, 0, s>>>(tt, tiled_stride_s, tiled_stride_h, scatter_index,
+                                             slot_valid, heads, n_heads, oo, out_rows, out_heads,
+                                             out_stride_s, out_stride_h);
+  else
+    scatter_kernel<64><<<grid, 256, 0, s>>>(tt, tiled_stride_s, tiled_stride_h, scatter_index,
+                                            slot_valid, heads, n_heads, oo, out_rows, out_heads,
+                                            out_stride_s, out_stride_h);
+  return check_launch("veda_scatter_tiles");
+}
+
+extern "C" int veda_gather_lse(const float* lse, int64_t lse_rows, int64_t lse_heads,
+                               int64_t lse_stride_s, int64_t lse_stride_h,
+                               const int64_t* gather_index, const int32_t* slot_valid,
+                               int64_t n_slots, const int64_t* heads, int64_t n_heads,
+                               float* out, void* stream) {
+  VEDA_REQUIRE(n_slots >= 0 && n_heads >= 0, "gather_lse: negative size");
+  const int64_t total = n_slots * n_heads;
+  if (total == 0) return VEDA_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  gather_lse_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
+      lse, lse_rows, lse_heads, lse_stride_s, lse_stride_h, gather_index, slot_valid, n_slots,
+      heads, n_heads, out);
+  return check_launch("veda_gather_lse");
+}

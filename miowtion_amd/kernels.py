@@ -1,0 +1,151 @@
+"""Layout-level entry points of the HIP kernels, with the reference's
+signatures:
+
+  gather_tiles / gather_and_pool / scatter_tiles_
+      miowtion/kernels/tile_gather_triton.py:156-224
+  pool_tiles                      miowtion/veda/predictor.py:82-130
+  gather_lse                      miowtion/veda/attention.py:299-305
+  index_lists                     miowtion/kernels/fa4.py:275-296
+  block_sparse_attention          miowtion/kernels/fa4.py:299-377
+  dense_attention                 miowtion/h3/attention.py:28-102
+  teacher_heat                    miowtion/kernels/block_heat_triton.py:141-173
+
+All run on the GPU through `miowtion_amd.ops`; CPU tensors raise
+NotImplementedError (no fallback, never a silent dense path).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from miowtion_amd import ops
+from miowtion_amd import tiling
+
+SECOND_RAW = 'raw'
+SECOND_CENTRAL = 'central'
+
+
+def supports(x: torch.Tensor) -> bool:
+    """The kernels can take this tensor (tile_gather_triton.py:55-66)."""
+    from miowtion_amd import _native
+    try:
+        _native.load()
+    except ImportError:
+        return False
+    return (x.is_cuda and x.dtype == torch.bfloat16 and x.shape[-1] in (64, 128)
+            and x.stride(-1) == 1)
+
+
+def _heads(x: torch.Tensor, heads: torch.Tensor | None) -> torch.Tensor:
+    if heads is None:
+        return torch.arange(x.shape[1], device=x.device)
+    return heads
+
+
+def gather_tiles(x: torch.Tensor, layout: tiling.TileLayout,
+                 heads: torch.Tensor | None) -> torch.Tensor:
+    """[S, H, D] -> [N, H', D] tile order, padding slots zero."""
+    return ops.gather(x, layout.gather_index, layout.slot_valid, layout.valid_count,
+                      _heads(x, heads), True, False, False)[0]
+
+
+def gather_and_pool(x: torch.Tensor, layout: tiling.TileLayout,
+                    heads: torch.Tensor | None, second: bool = False) -> tuple:
+    """gather_tiles and the predictor pooling in one pass over x.
+
+    Returns (rows [N, H', D], feats [H', n, 3D] fp32) plus
+    (E[x^2], Var(x)) [H', n, D] fp32 when `second`.
+    """
+    res = ops.gather(x, layout.gather_index, layout.slot_valid, layout.valid_count,
+                     _heads(x, heads), True, True, second)
+    return tuple(res)
+
+
+def pool_tiles(x: torch.Tensor, layout: tiling.TileLayout, second: str | None = None) -> torch.Tensor:
+    """Pooling of already tile-ordered rows [N, H', D] (predictor.py:82-130):
+    [H', n, 3D] fp32 [mean | max | min], or [H', n, D] E[x^2] ('raw') /
+    centred Var(x) ('central')."""
+    if second not in (None, SECOND_RAW, SECOND_CENTRAL):
+        raise ValueError(f'unknown second moment {second!r}')
+    ident = _identity(layout, x.device)
+    res = ops.gather(x, ident, layout.slot_valid, layout.valid_count,
+                     torch.arange(x.shape[1], device=x.device), False, True, second is not None)
+    if second is None:
+        return res[1]
+    return res[2] if second == SECOND_RAW else res[3]
+
+
+_IDENT: dict = {}
+
+
+def _identity(layout: tiling.TileLayout, device) -> torch.Tensor:
+    key = (layout.num_slots, str(device))
+    if key not in _IDENT:
+        _IDENT[key] = torch.arange(layout.num_slots, device=device)
+    return _IDENT[key]
+
+
+def scatter_tiles_(out: torch.Tensor, tiled: torch.Tensor, layout: tiling.TileLayout,
+                   heads: torch.Tensor | None) -> None:
+    """Writes tile-ordered rows into out[S + 1, H, D] (padding slots dropped)."""
+    if out.shape[0] != layout.seq_len + 1:
+        raise ValueError(f'scatter buffer needs {layout.seq_len + 1} rows')
+    ops.scatter_(out, tiled, layout.scatter_index, layout.slot_valid, _heads(out, heads))
+
+
+def gather_lse(lse: torch.Tensor, layout: tiling.TileLayout, heads: torch.Tensor) -> torch.Tensor:
+    """[S, H] LSE -> [N, H'] tile order, 0 on padding slots."""
+    return ops.gather_lse(lse, layout.gather_index, layout.slot_valid, heads)
+
+
+def index_lists(block_mask: torch.Tensor, layout: tiling.TileLayout) -> tuple[torch.Tensor, ...]:
+    """(partial_cnt, partial_idx, full_cnt, full_idx): cnt [1, H', R] and idx
+    [1, H', R, n] int32, members ascending then non-members ascending."""
+    return tuple(ops.index_lists(block_mask, layout.kv_ok, layout.full_tile))
+
+
+def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                           block_mask: torch.Tensor, layout: tiling.TileLayout,
+                           return_lse: bool = False):
+    """Block-sparse attention on tile-ordered tensors (fa4.py:299-377).
+
+    Args:
+        q: [R * 128, H', D] bf16 query tiles (rows of `block_mask`).
+        k, v: [N, H', D] bf16, all key tiles.
+        block_mask: [H', R, n_tiles] bool.
+        layout: Tile layout (valid key prefix of every key tile).
+        return_lse: Also return the [H', R * 128] fp32 natural-log LSE.
+
+    Returns:
+        [R * 128, H', D] bf16, or (out, lse).
+    """
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        raise NotImplementedError('the block-sparse backward is not part of this build')
+    lists = index_lists(block_mask, layout)
+    return block_sparse_attention_lists(q, k, v, lists, layout, return_lse)
+
+
+def block_sparse_attention_lists(q, k, v, lists, layout: tiling.TileLayout,
+                                 return_lse: bool = False):
+    """Same as block_sparse_attention with prebuilt (part_cnt, part_idx,
+    full_cnt, full_idx) lists (the BlockSparseTensorsTorch path of fa4.py)."""
+    part_cnt, part_idx, full_cnt, full_idx = lists
+    res = ops.block_sparse_fwd(q, k, v, part_cnt, part_idx, full_cnt, full_idx,
+                               layout.valid_count, return_lse)
+    return (res[0], res[1]) if return_lse else res[0]
+
+
+def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, used: int,
+                    return_lse: bool = False):
+    """Dense attention of rows [0, used) among themselves (h3/attention.py:28-102):
+    out [S, H, D] zero on padding rows, lse [S, H] fp32 (0 on padding) or None."""
+    res = ops.dense_fwd(q, k, v, used, return_lse)
+    return (res[0], res[1]) if return_lse else (res[0], None)
+
+
+def teacher_heat(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor,
+                 layout: tiling.TileLayout, q_tiles: torch.Tensor,
+                 reduce: str = 'max') -> torch.Tensor:
+    """[H', R, n_tiles] fp32 block heat ('max' peak / 'sum' mass) of query
+    tiles `q_tiles` (heatmap.py:36-110)."""
+    return ops.block_heat(q, k, lse, layout.slot_valid, q_tiles, reduce)

@@ -1,0 +1,101 @@
+"""Oracle: masked-dense block-sparse attention, dense attention with LSE and
+the teacher block heat (CPU torch, fp32 math, test-only).
+
+Restates:
+  * block_sparse_attention  -> `miowtion/kernels/reference.py:23-56`
+  * _math_attention / dense_attention (math backend)
+                            -> `miowtion/h3/attention.py:18-25,80-102`
+  * teacher_heat_reference  -> `miowtion/veda/heatmap.py:36-99`
+
+The reference materialises [H', N, N]; this restatement does the same math
+per head and per chunk of query rows so that C2-sized heads fit in memory.
+Heads and query rows are independent, so chunking changes no value.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from oracle.tiling import TILE, Layout
+
+
+def block_sparse_attention(q, k, v, block_mask, valid_count, return_lse=False,
+                           q_chunk: int = 1024):
+    """q [R*128, H', D], k/v [N, H', D], block_mask [H', R, n] -> out in
+    q.dtype (and lse [H', R*128] fp32, -inf for rows with no key)."""
+    Rq, H, D = q.shape
+    N = k.shape[0]
+    scale = 1.0 / math.sqrt(D)
+    key_valid = (torch.arange(TILE)[None, :] < valid_count[:, None]).reshape(-1)[:N]
+    out = torch.empty(Rq, H, D, dtype=torch.float32)
+    lse = torch.empty(H, Rq, dtype=torch.float32)
+    kf, vf = k.float(), v.float()
+    for h in range(H):
+        bm = block_mask[h]
+        for q0 in range(0, Rq, q_chunk):
+            q1 = min(q0 + q_chunk, Rq)
+            rows = torch.arange(q0, q1) // TILE
+            tok = bm[rows].repeat_interleave(TILE, 1)[:, :N] & key_valid[None, :]
+            s = (q[q0:q1, h].float() @ kf[:, h].T) * scale
+            s = s.masked_fill(~tok, float('-inf'))
+            p = torch.softmax(s, -1).nan_to_num(0.0)
+            out[q0:q1, h] = p @ vf[:, h]
+            lse[h, q0:q1] = torch.logsumexp(s, -1)
+    o = out.to(q.dtype)
+    return (o, lse) if return_lse else o
+
+
+def dense_attention(q, k, v, used: int, return_lse=False, q_chunk: int = 1024):
+    """h3/attention.py 'math' backend: rows [0, used) attend among themselves;
+    out zero and lse 0 on padding rows. q/k/v [S, H, D]; lse [S, H]."""
+    S, H, D = q.shape
+    scale = 1.0 / math.sqrt(D)
+    out = torch.zeros(S, H, D, dtype=torch.float32)
+    lse = torch.zeros(S, H, dtype=torch.float32)
+    kf, vf = k[:used].float(), v[:used].float()
+    for h in range(H):
+        for q0 in range(0, used, q_chunk):
+            q1 = min(q0 + q_chunk, used)
+            s = (q[q0:q1, h].float() @ kf[:, h].T) * scale
+            l = torch.logsumexp(s, -1)
+            out[q0:q1, h] = torch.exp(s - l[:, None]) @ vf[:, h]
+            lse[q0:q1, h] = l
+    o = out.to(q.dtype)
+    return (o, lse) if return_lse else (o, None)
+
+
+def teacher_heat(q, k, lse, lay: Layout, q_tiles, reduce='sum', score_dtype=torch.float32):
+    """heatmap.py:36-99 -> [H', R, n] fp32.
+
+    score_dtype=torch.bfloat16 reproduces the reference's torch path, whose
+    bf16 `bmm` rounds every score; torch.float32 keeps the scores in fp32
+    (what an MFMA kernel with fp32 accumulation computes).
+    """
+    if reduce not in ('max', 'sum'):
+        raise ValueError(f"reduce must be 'max' or 'sum': {reduce!r}")
+    H, D = q.shape[1], q.shape[2]
+    scale = 1.0 / math.sqrt(D)
+    valid = lay.slot_valid.bool()
+    n = lay.n_tiles
+    heat = torch.zeros(H, q_tiles.numel(), n, dtype=torch.float32)
+    kf = k.float()
+    for ri, r in enumerate(q_tiles.tolist()):
+        rows = torch.arange(r * TILE, (r + 1) * TILE)
+        row_ok = valid[rows]
+        for h in range(H):
+            s = q[rows, h].float() @ kf[:, h].T
+            s = s.to(score_dtype).float()
+            s = s.masked_fill(~valid[None, :], float('-inf'))
+            blocks = s.view(TILE, n, TILE)
+            l = lse[rows, h]
+            if reduce == 'max':
+                m = torch.exp(blocks.amax(-1) * scale - l[:, None])
+                m = m.masked_fill(~row_ok[:, None], 0.0)
+                heat[h, ri] = m.amax(0)
+            else:
+                p = torch.exp(blocks * scale - l[:, None, None]).sum(-1)
+                p = p.masked_fill(~row_ok[:, None], 0.0)
+                heat[h, ri] = p.sum(0)
+    return heat

@@ -1,0 +1,156 @@
+"""GPU parity of the block-sparse and dense attention forwards against the
+fp32 masked-dense oracle. Bar: on real rows, output
+max-abs <= 2e-2 and rel-L2 <= 1e-2 (bf16 I/O); LSE to the same max-abs."""
+
+import pytest
+import torch
+
+from miowtion_amd import kernels
+from miowtion_amd import mask as pm
+from oracle import attention as oa
+from oracle import mask as om
+from oracle import tiling as ot
+from tests import helpers
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+REL_L2 = 1e-2
+
+
+def _close(got, want, rows=None):
+    got, want = got.float().cpu(), want.float().cpu()
+    if rows is not None:
+        got, want = got[rows], want[rows]
+    fin = torch.isfinite(want)
+    assert torch.equal(torch.isfinite(got), fin)
+    assert torch.equal(got[~fin], want[~fin])
+    err = (got[fin] - want[fin]).abs().max().item() if fin.any() else 0.0
+    rel = ((got[fin] - want[fin]).norm() / want[fin].norm().clamp(min=1e-30)).item()
+    assert err <= MAX_ABS, f'max-abs {err}'
+    assert rel <= REL_L2, f'rel-L2 {rel}'
+    return err, rel
+
+
+def _case(spec, heads=4, ratio=0.3, seed=0):
+    lay = helpers.product_layout(*spec, device='cuda')
+    olay = helpers.oracle_layout(*spec)
+    q, k, v = helpers.qkv(lay.seq_len, heads, 128, seed=seed)
+    qt, kt, vt = (ot.gather_tiles(t, olay, None) for t in (q, k, v))
+    scores = torch.randn(heads, lay.n_tiles, lay.n_tiles, generator=torch.Generator().manual_seed(seed + 1))
+    idx, keep = om.select_video_blocks(scores[:, :lay.n_video_tiles], olay,
+                                       om.column_blocks(olay, om.Budget(ratio=ratio)))
+    mask = om.dense_block_mask(idx, keep, olay)
+    return lay, olay, qt, kt, vt, mask
+
+
+def test_sparse_matches_oracle_with_partial_tiles():
+    # reference tests/gpu/test_kernels_gpu.py:95-112
+    lay, olay, qt, kt, vt, mask = _case(helpers.small_layout())
+    assert olay.partial_tiles.numel() > 0
+    out, lse = kernels.block_sparse_attention(qt.cuda(), kt.cuda(), vt.cuda(), mask.cuda(), lay,
+                                              return_lse=True)
+    ref, ref_lse = oa.block_sparse_attention(qt, kt, vt, mask, olay.valid_count, return_lse=True)
+    real = olay.slot_valid.bool()
+    _close(out, ref, real)
+    _close(lse.T, ref_lse.T, real)
+
+
+def test_keep_all_sparse_equals_dense_kernel_and_oracle():
+    # reference tests/gpu/test_kernels_gpu.py:115-138
+    spec = helpers.small_layout()
+    lay, olay, qt, kt, vt, _ = _case(spec)
+    mask = torch.ones(4, lay.n_tiles, lay.n_tiles, dtype=torch.bool)
+    out = kernels.block_sparse_attention(qt.cuda(), kt.cuda(), vt.cuda(), mask.cuda(), lay)
+    ref = oa.block_sparse_attention(qt, kt, vt, mask, olay.valid_count)
+    real = olay.slot_valid.bool()
+    _close(out, ref, real)
+
+
+def test_empty_query_tiles_give_zero_and_neg_inf_lse():
+    lay, olay, qt, kt, vt, mask = _case(helpers.small_layout(), ratio=0.5)
+    mask[1, 3] = False
+    mask[0, :, :] = False
+    out, lse = kernels.block_sparse_attention(qt.cuda(), kt.cuda(), vt.cuda(), mask.cuda(), lay,
+                                              return_lse=True)
+    out, lse = out.cpu(), lse.cpu()
+    assert (out[:, 0] == 0).all() and torch.isinf(lse[0]).all() and (lse[0] < 0).all()
+    assert (out[3 * 128:4 * 128, 1] == 0).all() and (lse[1, 3 * 128:4 * 128] == float('-inf')).all()
+    ref, ref_lse = oa.block_sparse_attention(qt, kt, vt, mask, olay.valid_count, return_lse=True)
+    real = olay.slot_valid.bool()
+    _close(out, ref, real)
+    _close(lse.T, ref_lse.T, real)
+
+
+def test_query_tile_subset_rows():
+    """q holds only some query tiles; mask rows follow q (fa4.py:308-313)."""
+    lay, olay, qt, kt, vt, mask = _case(helpers.small_layout(), seed=3)
+    rows = torch.tensor([1, 4, 5])
+    qs = qt.view(-1, 128, 4, 128)[rows].reshape(-1, 4, 128)
+    ms = mask[:, rows]
+    out = kernels.block_sparse_attention(qs.cuda(), kt.cuda(), vt.cuda(), ms.cuda(), lay)
+    ref = oa.block_sparse_attention(qs, kt, vt, ms, olay.valid_count)
+    real = olay.slot_valid.view(-1, 128)[rows].reshape(-1).bool()
+    _close(out, ref, real)
+
+
+def test_config1_end_to_end_blocks_and_attention():
+    """8 heads, grid 4x16x16 -> 8 tiles (2,8,8), uniform
+    random tile scores, top 50% per query tile with the diagonal."""
+    spec = helpers.CONFIGS['C1']
+    lay = helpers.product_layout(*spec, device='cuda')
+    olay = helpers.oracle_layout(*spec)
+    q, k, v = helpers.qkv(1024, 8, 128, seed=0)
+    scores = torch.rand(8, 8, 8, generator=torch.Generator().manual_seed(1))
+    sel = pm.select_video_blocks(scores.cuda(), lay, pm.column_blocks(lay, pm.Budget(ratio=0.5)))
+    idx, keep = om.select_video_blocks(scores, olay, om.column_blocks(olay, om.Budget(ratio=0.5)))
+    assert torch.equal(sel.index.cpu(), idx) and torch.equal(sel.keep.cpu(), keep)
+    mask = pm.dense_block_mask(sel, lay)
+    assert (mask.sum(-1) == 4).all()
+    qt, kt, vt = (kernels.gather_tiles(t.cuda(), lay, None) for t in (q, k, v))
+    out, lse = kernels.block_sparse_attention(qt, kt, vt, mask, lay, return_lse=True)
+    oq, ok, ov = (ot.gather_tiles(t, olay, None) for t in (q, k, v))
+    ref, ref_lse = oa.block_sparse_attention(oq, ok, ov, mask.cpu(), olay.valid_count, return_lse=True)
+    _close(out, ref)
+    _close(lse, ref_lse)
+
+
+@pytest.mark.parametrize('seq_len,used', [(2048, 2000), (1000, 1000), (64 * 21, 64 * 21 - 7)])
+def test_dense_matches_oracle(seq_len, used):
+    # reference tests/gpu/test_kernels_gpu.py:32-41
+    q, k, v = helpers.qkv(seq_len, 4, 128)
+    out, lse = kernels.dense_attention(q.cuda(), k.cuda(), v.cuda(), used, return_lse=True)
+    ref, ref_lse = oa.dense_attention(q, k, v, used, return_lse=True)
+    _close(out, ref)
+    _close(lse, ref_lse)
+    assert (out[used:] == 0).all() and (lse[used:] == 0).all()
+
+
+def test_sampled_query_tiles_at_config2_size():
+    """C2 geometry (592 tiles, 48 heads) at 90% sparsity: sampled query tiles
+    of the full-size kernel call against the oracle (size-independent check:
+    every row's output is a convex combination of its kept values)."""
+    spec = helpers.CONFIGS['C2']
+    lay = helpers.product_layout(*spec, device='cuda')
+    olay = helpers.oracle_layout(*spec)
+    H = 48
+    g = torch.Generator(device='cuda').manual_seed(0)
+    q, k, v = (torch.randn(lay.seq_len, H, 128, generator=g, device='cuda').to(torch.bfloat16)
+               for _ in range(3))
+    qt, kt, vt = (kernels.gather_tiles(t, lay, None) for t in (q, k, v))
+    scores = torch.rand(H, lay.n_tiles, lay.n_tiles, generator=g, device='cuda')
+    sel = pm.select_video_blocks(scores, lay, pm.column_blocks(lay, pm.Budget(ratio=0.1)))
+    mask = pm.dense_block_mask(sel, lay)
+    out, lse = kernels.block_sparse_attention(qt, kt, vt, mask, lay, return_lse=True)
+    assert torch.isfinite(out.float()).all()
+    rows = torch.tensor([0, 17, 333, 591])
+    heads = [0, 47]
+    sub_q = qt.view(-1, 128, H, 128)[rows.cuda()].reshape(-1, H, 128)[:, heads].cpu()
+    sub_m = mask[heads][:, rows.cuda()].cpu()
+    ref, ref_lse = oa.block_sparse_attention(sub_q, kt[:, heads].cpu(), vt[:, heads].cpu(), sub_m,
+                                             olay.valid_count, return_lse=True)
+    got = out.view(-1, 128, H, 128)[rows.cuda()].reshape(-1, H, 128)[:, heads]
+    got_lse = lse.view(H, -1, 128)[heads][:, rows.cuda()].reshape(len(heads), -1)
+    real = olay.slot_valid.view(-1, 128)[rows].reshape(-1).bool()
+    _close(got, ref, real)
+    _close(got_lse.T, ref_lse.T, real)

@@ -1,0 +1,134 @@
+"""GPU parity of the teacher block heat and the predictor scoring.
+
+Heat: against the oracle with fp32 scores (the kernel accumulates QK^T in
+fp32) to 1e-4 relative for 'sum' and, like the
+reference's own GPU test (tests/gpu/test_kernels_gpu.py:44-78), to 3e-2
+against the bf16-score torch form. Predictor: fp32 logits to 1e-4 relative;
+the selection from the kernel's logits is bit-exact to the oracle's selection
+on the same logits."""
+
+import math
+
+import pytest
+import torch
+
+from miowtion_amd import kernels
+from miowtion_amd import mask as pm
+from miowtion_amd import ops
+from miowtion_amd import predictor as pp
+from oracle import attention as oa
+from oracle import mask as om
+from oracle import predictor as op
+from oracle import tiling as ot
+from tests import helpers
+
+pytestmark = pytest.mark.gpu
+
+
+def _heat_case():
+    spec = helpers.small_layout()
+    lay = helpers.product_layout(*spec, device='cuda')
+    olay = helpers.oracle_layout(*spec)
+    q, k, v = helpers.qkv(lay.seq_len, 4, 128)
+    _, lse = oa.dense_attention(q, k, v, lay.used, return_lse=True)
+    heads = torch.arange(4)
+    qt, kt = (ot.gather_tiles(t, olay, heads) for t in (q, k))
+    lse_t = ot.gather_lse(lse, olay, heads)
+    rows = torch.arange(0, lay.n_tiles, 3)
+    return lay, olay, qt, kt, lse_t, rows
+
+
+@pytest.mark.parametrize('reduce', ['sum', 'max'])
+def test_heat_matches_oracle(reduce):
+    lay, olay, qt, kt, lse_t, rows = _heat_case()
+    got = kernels.teacher_heat(qt.cuda(), kt.cuda(), lse_t.cuda(), lay, rows.cuda(), reduce).cpu()
+    ref32 = oa.teacher_heat(qt, kt, lse_t, olay, rows, reduce, score_dtype=torch.float32)
+    ref16 = oa.teacher_heat(qt, kt, lse_t, olay, rows, reduce, score_dtype=torch.bfloat16)
+    if reduce == 'sum':
+        torch.testing.assert_close(got, ref32, rtol=1e-4, atol=1e-7)
+    else:
+        # the kernel rounds the row max to bf16 exactly as the reference does
+        torch.testing.assert_close(got, ref16, rtol=2e-3, atol=1e-7)
+    torch.testing.assert_close(got, ref16, rtol=3e-2, atol=1e-5)
+    if reduce == 'sum':
+        want = olay.valid_count[rows].float()
+        torch.testing.assert_close(got.sum(-1), want.expand(4, -1), rtol=1e-3, atol=1e-3)
+
+
+def test_heat_rejects_unknown_reduction():
+    lay, _, qt, kt, lse_t, rows = _heat_case()
+    with pytest.raises(ValueError, match='reduce must be'):
+        kernels.teacher_heat(qt.cuda(), kt.cuda(), lse_t.cuda(), lay, rows.cuda(), 'mean')
+
+
+def _predictor_case(fp8, second=0, count=False, seed=0):
+    spec = helpers.small_layout()
+    lay = helpers.product_layout(*spec, device='cuda')
+    olay = helpers.oracle_layout(*spec)
+    q, k = helpers.qkv(lay.seq_len, 6, 128, seed=seed, n=2)
+    heads = torch.tensor([4, 1, 2])
+    g = torch.Generator().manual_seed(seed + 10)
+    pred = pp.LayerPredictor.random(6, 128, std=0.02, generator=g, device='cuda', fp8=fp8,
+                                    second_order_rank=second, count_term=count)
+    if count:
+        pred.count_gain = torch.tensor([0.5, 1.0, 1.5, 2.0, 0.25, 3.0], device='cuda')
+    return lay, olay, q, k, heads, pred
+
+
+def _oracle_weight(w: pp.ProjWeight):
+    if w.scale is not None:
+        return op.dequantize_fp8(w.values.cpu(), w.scale.cpu())
+    return w.values.cpu()
+
+
+@pytest.mark.parametrize('fp8', [False, True])
+@pytest.mark.parametrize('second,count', [(0, False), (16, True)])
+def test_predictor_logits_match_oracle(fp8, second, count):
+    lay, olay, q, k, heads, pred = _predictor_case(fp8, second, count)
+    want_second = bool(second)
+    if want_second:
+        qt, fq, sq, _ = kernels.gather_and_pool(q.cuda(), lay, heads.cuda(), second=True)
+        kt, fk, _, vk = kernels.gather_and_pool(k.cuda(), lay, heads.cuda(), second=True)
+    else:
+        qt, fq = kernels.gather_and_pool(q.cuda(), lay, heads.cuda())
+        kt, fk = kernels.gather_and_pool(k.cuda(), lay, heads.cuda())
+        sq = vk = None
+    extra = {}
+    if count:
+        extra['log_count'] = pp.log_count(lay)
+    if want_second:
+        extra['sq_q'], extra['var_k'] = sq, vk
+    got = pred(fq, fk, heads.cuda(), **extra).cpu()
+    oq, ok = ot.gather_tiles(q, olay, heads), ot.gather_tiles(k, olay, heads)
+    ofq, ofk = op.pool_tiles(oq, olay), op.pool_tiles(ok, olay)
+    kw = {}
+    if count:
+        kw.update(gain=pred.count_gain.cpu(), log_count=torch.log(olay.valid_count.clamp(min=1).float()))
+    if want_second:
+        kw.update(sq_q=op.pool_tiles(oq, olay, 'raw'), var_k=op.pool_tiles(ok, olay, 'central'),
+                  so_q=_oracle_weight(pred.so_q), so_k=_oracle_weight(pred.so_k))
+    want = op.logits(ofq, ofk, _oracle_weight(pred.proj_q), _oracle_weight(pred.proj_k), heads, **kw)
+    scale = want.abs().max()
+    assert (got - want).abs().max() <= 1e-4 * scale + 1e-6
+    # selection from the kernel's logits == oracle selection on those logits
+    sel = pm.select_video_blocks(got[:, :lay.n_video_tiles].cuda(), lay,
+                                 pm.column_blocks(lay, pm.Budget(ratio=0.3)))
+    idx, keep = om.select_video_blocks(got[:, :lay.n_video_tiles], olay,
+                                       om.column_blocks(olay, om.Budget(ratio=0.3)))
+    assert torch.equal(sel.index.cpu(), idx) and torch.equal(sel.keep.cpu(), keep)
+
+
+def test_e4m3_decode_matches_torch_for_every_code():
+    """Every finite e4m3 code decodes as torch's float8_e4m3fn does (the two
+    NaN codes are left out: a NaN weight poisons its whole output column)."""
+    codes = torch.arange(256, dtype=torch.uint8)
+    codes[127] = 0
+    codes[255] = 0
+    vals = codes.view(torch.float8_e4m3fn)
+    w = vals.view(1, 16, 16).cuda()
+    scale = torch.ones(1, device='cuda')
+    feats = torch.eye(16, device='cuda')[None]
+    got = ops.predictor_embed(feats, w, scale, torch.zeros(1, dtype=torch.long, device='cuda'),
+                              False).cpu()[0]
+    want = vals.float().to(torch.bfloat16).float().view(16, 16)
+    assert torch.equal(got, want)

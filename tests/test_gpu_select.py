@@ -1,0 +1,103 @@
+"""GPU parity of the top-k selection, the block mask and the full / partial
+lists: bit-exact against the oracle (which equals torch.topk on distinct
+scores and follows the stable order on ties)."""
+
+import math
+
+import pytest
+import torch
+
+from miowtion_amd import kernels
+from miowtion_amd import mask as pm
+from oracle import mask as om
+from oracle import tiling as ot
+from tests import helpers
+
+pytestmark = pytest.mark.gpu
+
+
+def _spec_with_cond():
+    # condition span (tiled with its least-padding shape in the reference's
+    # ClipTiling) + target: two column blocks with their own budgets
+    return [(90, (1, 16, 32)), (90 + 512 + 40, (16, 8, 16))], 90 + 512 + 40 + 2048, 90 + 512 + 40 + 2048, '4x8x4'
+
+
+def _layouts(spec):
+    return helpers.product_layout(*spec, device='cuda'), helpers.oracle_layout(*spec)
+
+
+def _run(scores, lay, olay, p_blocks, o_blocks, rows=None):
+    sel = pm.select_video_blocks(scores.cuda(), lay, p_blocks, None if rows is None else rows.cuda())
+    ri, rk = om.select_video_blocks(scores, olay, o_blocks, rows)
+    assert torch.equal(sel.index.cpu(), ri)
+    assert torch.equal(sel.keep.cpu(), rk)
+    return sel, ri, rk
+
+
+@pytest.mark.parametrize('seed', range(3))
+def test_select_bit_exact_two_blocks(seed):
+    lay, olay = _layouts(_spec_with_cond())
+    nv = lay.n_video_tiles
+    g = torch.Generator().manual_seed(seed)
+    scores = torch.randn(3, nv, lay.n_tiles, generator=g)
+    pb = pm.column_blocks(lay, pm.Budget(ratio=0.25), pm.Budget(tiles=2.5))
+    ob = om.column_blocks(olay, om.Budget(ratio=0.25), om.Budget(tiles=2.5))
+    sel, ri, rk = _run(scores, lay, olay, pb, ob)
+    mask = pm.dense_block_mask(sel, lay).cpu()
+    assert torch.equal(mask, om.dense_block_mask(ri, rk, olay))
+    rows = torch.tensor([0, lay.n_ref_tiles - 1, lay.n_ref_tiles, nv - 1])
+    sel, ri, rk = _run(scores[:, rows], lay, olay, pb, ob, rows)
+    sub = pm.dense_block_mask(sel, lay, global_rows=False).cpu()
+    assert torch.equal(sub, om.dense_block_mask(ri, rk, olay, global_rows=False))
+
+
+def test_select_ties_follow_the_stable_order():
+    lay, olay = _layouts(_spec_with_cond())
+    nv = lay.n_video_tiles
+    scores = torch.randint(0, 4, (3, nv, lay.n_tiles), generator=torch.Generator().manual_seed(0)).float()
+    scores[0, :, 5] = -0.0
+    scores[0, :, 6] = 0.0
+    pb = pm.column_blocks(lay, pm.Budget(ratio=0.25), pm.Budget(tiles=2))
+    ob = om.column_blocks(olay, om.Budget(ratio=0.25), om.Budget(tiles=2))
+    _run(scores, lay, olay, pb, ob)
+
+
+def test_select_keep_all_and_budget_above_columns():
+    lay, olay = _layouts(helpers.small_layout())
+    scores = torch.rand(2, lay.n_video_tiles, lay.n_tiles, generator=torch.Generator().manual_seed(3))
+    for b in (1.0, 0.999):
+        _run(scores, lay, olay, pm.column_blocks(lay, pm.Budget(ratio=b)),
+             om.column_blocks(olay, om.Budget(ratio=b)))
+    _run(scores, lay, olay, pm.column_blocks(lay, pm.Budget(tiles=1000)),
+         om.column_blocks(olay, om.Budget(tiles=1000)))
+
+
+def test_index_lists_bit_exact():
+    lay, olay = _layouts(helpers.small_layout())
+    g = torch.Generator().manual_seed(5)
+    mask = torch.rand(4, lay.n_tiles, lay.n_tiles, generator=g) < 0.4
+    got = kernels.index_lists(mask.cuda(), lay)
+    want = om.index_lists(mask, olay)
+    for a, b in zip(got, want):
+        assert a.dtype == b.dtype and torch.equal(a.cpu(), b)
+
+
+@pytest.mark.parametrize('name,ratio', [('C2', 0.1), ('C3b', 0.2)])
+def test_selection_and_lists_at_full_size(name, ratio):
+    """48 heads of uniform random scores at the BASELINE geometry: top-k,
+    block mask and lists bit-exact; kept blocks per head = the equal-cost
+    budget (C2: 20,340, C3: 40,680)."""
+    lay, olay = _layouts(helpers.CONFIGS[name])
+    n = lay.n_tiles
+    scores = torch.rand(48, n, n, generator=torch.Generator().manual_seed(11))
+    pb = pm.column_blocks(lay, pm.Budget(ratio=ratio))
+    ob = om.column_blocks(olay, om.Budget(ratio=ratio))
+    sel, ri, rk = _run(scores, lay, olay, pb, ob)
+    mask = pm.dense_block_mask(sel, lay)
+    want_mask = om.dense_block_mask(ri, rk, olay)
+    assert torch.equal(mask.cpu(), want_mask)
+    expected = {'C2': 20340, 'C3b': 40680}[name]
+    assert (mask.sum((1, 2)).cpu() == expected).all()
+    got = kernels.index_lists(mask, lay)
+    for a, b in zip(got, om.index_lists(want_mask, olay)):
+        assert torch.equal(a.cpu(), b)

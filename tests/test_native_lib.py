@@ -1,0 +1,60 @@
+"""The C ABI: libveda_hip.so loads, exports every entry point declared in
+include/veda_hip.h with the arity the ctypes binding uses, and rejects bad
+arguments on the host before any launch (these paths make no HIP call, so
+they run without a GPU)."""
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from miowtion_amd import _native
+
+HEADER = pathlib.Path(__file__).resolve().parent.parent / 'include' / 'veda_hip.h'
+
+
+def _declared():
+    text = re.sub(r'/\*.*?\*/', '', HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r'\b(?:int|const char\*)\s+(veda_\w+)\s*\(([^;]*?)\)\s*;', text, re.S):
+        args = [a.strip() for a in m.group(2).split(',') if a.strip() and a.strip() != 'void']
+        out[m.group(1)] = len(args)
+    return out
+
+
+def test_library_built_and_exports_every_declared_symbol():
+    lib = _native.load()
+    declared = _declared()
+    assert {'veda_gather_tiles', 'veda_block_sparse_fwd', 'veda_block_heat',
+            'veda_select_topk', 'veda_index_lists'} <= set(declared)
+    for name in declared:
+        assert hasattr(lib, name), name
+    # the binding covers every compute entry point with the declared arity
+    for name, n in declared.items():
+        if name in ('veda_last_error', 'veda_abi_version'):
+            continue
+        assert len(_native.SIGNATURES[name]) == n, name
+    assert set(_native.SIGNATURES) <= set(declared)
+    assert lib.veda_abi_version() == 1
+
+
+def test_host_side_argument_checks():
+    lib = _native.load()
+    # head_dim 96 is refused before anything is launched
+    with pytest.raises(ValueError, match='head_dim'):
+        _native.call('veda_gather_tiles', None, 0, 0, 0, 0, None, None, None, 1, None, 1, 96,
+                     None, 0, 0, None, None, None, None)
+    with pytest.raises(ValueError, match='k_lo'):
+        _native.call('veda_select_topk', None, 1, 1, 0, 0, 0, 10, None, None, 5, 4, None, 0,
+                     None, None, 0, 0, 0, None)
+    with pytest.raises(ValueError, match='head_dim'):
+        _native.call('veda_block_sparse_fwd', None, 0, 0, None, 0, 0, None, 0, 0, 1, 64, 1, 1,
+                     None, None, None, None, 1, None, 1.0, None, 0, 0, None, 0, 0, None)
+    with pytest.raises(ValueError, match='reduce'):
+        _native.call('veda_block_heat', None, 0, 0, None, 0, 0, None, 0, 0, None, None, 1, 1,
+                     1, 128, 3, 1.0, None, None)
+    with pytest.raises(ValueError, match='used'):
+        _native.call('veda_dense_fwd', None, 0, 0, None, 0, 0, None, 0, 0, 10, 11, 1, 128, 1.0,
+                     None, 0, 0, None, 0, 0, None)
+    assert isinstance(lib.veda_last_error(), bytes)
