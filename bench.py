@@ -143,6 +143,11 @@ def main() -> int:
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-dense', action='store_true')
     ap.add_argument('--cpu-budget', type=float, default=20.0)
+    ap.add_argument('--only-kernel', action='store_true',
+                    help='time the sparse forward only (for rocprofv3 runs)')
+    ap.add_argument('--copy-bytes', type=int, default=0,
+                    help='first run 3 device-to-device copies of this many bytes: the known-size '
+                         'reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only (asked for --gpus {args.gpus}); the Veda path '
@@ -150,6 +155,15 @@ def main() -> int:
               'shares -- run with --gpus 1', file=sys.stderr)
         return 2
     from miowtion_amd import kernels, mask as pm
+    if args.copy_bytes:
+        n = args.copy_bytes // 4
+        src = torch.ones(n, dtype=torch.float32, device='cuda')
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        _log(f'bench: copied {args.copy_bytes} bytes x 3 (counter calibration)')
     _log('bench: building C2 case')
     c = build_case()
     lay = c['lay']
@@ -175,6 +189,11 @@ def main() -> int:
     k_ms = kernel_ms[len(kernel_ms) // 2]
     k_avg = sum(kernel_ms) / len(kernel_ms)
     achieved = flop / (k_avg * 1e-3) / 1e12
+    if args.only_kernel:
+        print(json.dumps({'metric': METRIC, 'value': round(flop / (k_ms * 1e-3) / 1e12, 2),
+                          'ms_per_step': round(k_ms, 4), 'avg_launch_ms': round(k_avg, 4),
+                          'only_kernel': True}), flush=True)
+        return 0
 
     _log('bench: +prep and full layer')
     prep_ms = sorted(_events_ms(lambda: c['prep'](), 5))[2]
