@@ -2,11 +2,10 @@
 // fp32 accumulate), and the dense forward built from the same kernel.
 //
 // Workgroup = one (head, 128-row query tile), 8 waves, 1 workgroup per CU:
-//   wave w: query group qg = w % 4 (32 query rows), key half kh = w / 4
-//   (keys [64 kh, 64 kh + 64) of every 128-key block).
-// Two waves share each SIMD, so one wave's softmax overlaps the other's
-// MFMAs. The two key halves keep separate online-softmax states and are
-// merged through LDS at the end.
+//   wave w: query group qg = w & 3 (32 query rows), key half kh = w >> 2;
+//   waves w and w + 4 share a SIMD, so one wave's softmax can overlap the
+//   other's MFMAs. The two key halves keep separate online-softmax states
+//   and are merged through LDS at the end.
 //
 // Scores are computed transposed, S^T = K Q^T with v_mfma_f32_32x32x16_bf16
 // (A = K rows from LDS, B = Q^T held in registers), so every lane owns ONE
@@ -18,18 +17,16 @@
 // free: lane half h supplies keys 16s + 4h + {0..3, 8..11}, the order in
 // which the accumulator registers hold P^T.
 //
-// K and V tiles go from HBM straight into LDS (global_load_lds_dwordx4: lane
-// l of a wave writes bytes [16 l, 16 l + 16) of a 1 KB segment), two stages,
-// the next block's loads in flight while the current block is computed; no
-// register staging and no transposing stores. Both tiles keep their natural
-// [key][head_dim] row layout with the 16-byte chunks of row r permuted:
+// K and V go from HBM straight into LDS (global_load_lds_dwordx4: lane l of
+// a wave writes bytes [16 l, 16 l + 16) of a 1 KB segment), no register
+// staging and no transposing stores. Both keep their natural [key][head_dim]
+// row layout with the 16-byte chunks of row r permuted:
 //   K: chunk c at position c ^ (r & 15)   -> the 16-byte K fragment reads of
 //      32 consecutive rows are conflict-free;
 //   V: chunk c at position c ^ 4 (r & 3)  -> the V^T fragments, assembled by
 //      two ds_read_b64_tr_b16 (lane i of a 16-lane group receives element
 //      (i mod 4) of source lane 4 j + i / 4, j = 0..3), are conflict-free.
-// The walk over kept blocks is unrolled by two over two distinct LDS arrays,
-// so the DMA into one stage provably does not alias the reads of the other.
+// The pipeline over the kept blocks is described at the half-block section.
 
 #include "veda_common.h"
 
@@ -39,7 +36,6 @@ namespace {
 constexpr int kD = 128;
 constexpr int kThreads = 512;
 constexpr int kTileBytes = kTile * kD * 2;       // 32 KB: one K or V tile
-constexpr int kStageBytes = 2 * kTileBytes;      // K + V
 constexpr int kMaxBlocks = 2048;                 // key tiles per row (FA4's cap)
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleSlack = 8.f;             // log2 units
@@ -88,146 +84,224 @@ __device__ __forceinline__ float half_swap_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Issues the HBM -> LDS loads of block j into one stage: wave w fills K and
-// V segments 4w .. 4w+3 (rows 16w .. 16w+15); rows past kv_rows are clamped
-// (a clamped row only ever feeds masked keys).
-__device__ __forceinline__ void issue_stage(const FwdParams& p, int64_t head, int64_t j, int wave,
-                                            int lane, lds_u8* stage) {
-  const int64_t row0 = j * kTile;
-  const int64_t rem = p.kv_rows - 1 - row0;
-  const int last = rem < kTile - 1 ? (int)rem : kTile - 1;
-  const uint16_t* kbase = p.k + head * p.kh + row0 * p.ks;
-  const uint16_t* vbase = p.v + head * p.vh + row0 * p.vs;
-  const int ks = (int)p.ks, vs = (int)p.vs;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int seg = 4 * wave + u;
-    const int row = 4 * seg + (lane >> 4), pc = lane & 15;
-    const int src = min(row, last);
-    __builtin_amdgcn_global_load_lds(kbase + (src * ks + ((pc ^ (row & 15)) << 3)),
-                                     (lds_void*)(stage + seg * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(vbase + (src * vs + ((pc ^ ((row & 3) << 2)) << 3)),
-                                     (lds_void*)(stage + kTileBytes + seg * 1024), 16, 0, 0);
-  }
-}
-
-struct Walk {
-  const int32_t* j;   // LDS: key tile of every step
-  const int32_t* vc;  // LDS: valid keys of every step
-};
-
+// Per-wave state: Q^T fragments of the wave's 32 rows (lane (li, hi) holds
+// q[row 32 qg + li, 16 s + 8 hi .. + 7]), the O^T accumulators
+// (O^T[d in 32 dt .. + 31][row]) and the online-softmax state of its rows.
 struct WaveState {
   bf16x8 qf[8];
   f32x16 o[4];
   float m_run, l_run;
 };
 
-// One block (128 keys) of the online softmax for this wave's 32 rows and 64
-// keys, reading K and V from `stage`.
-__device__ __forceinline__ void attend_block(const FwdParams& p, const lds_u8* stage, int vc,
-                                             int kh, int li, int hi, int lane, WaveState& w) {
-  const lds_u8* kb = stage;
-  const lds_u8* vb = stage + kTileBytes;
-  // S^T: two 32-key sub-tiles, accumulator chains alternating.
-  f32x16 sacc[2];
+// ---------------------------------------------------------------------------
+// Half-block pipeline.
+//
+// The unit of the pipeline is a step: 64 keys of one key tile, K and V
+// together 32 KB. Four LDS slots form a ring, so three steps are in flight
+// while one is computed (96 KB per CU; with a random block list most K/V
+// reads miss L2 and come over the fabric, which needs that depth to run at
+// its bandwidth).
+//
+// A step loads and computes only what the key tile holds: rows at or past
+// the tile's valid count are padding (masked by definition), so their 1 KB
+// segments are not fetched (the load is redirected to rows already being
+// fetched, which keeps every wave's load count fixed for the vmcnt waits),
+// and the upper half of a tile with at most 64 valid keys is no step at all.
+// Stale LDS rows only ever meet masked keys (p = 0); the ring is zeroed once
+// so no uninitialised bits are ever multiplied.
+//
+// In each step wave (qg, kh) takes keys 32 kh .. 32 kh + 31 of the half:
+// S^T = K Q^T (8 MFMAs), one online-softmax step over its 32 keys, and
+// O^T += V^T P^T (8 MFMAs); a wave whose 32 keys are all padding skips the
+// step. The two key halves merge at the end.
+
+constexpr int kHalf = 64;                       // keys per step
+constexpr int kHalfBytes = kHalf * kD * 2;      // 16 KB: K or V of a step
+constexpr int kSlotBytes = 2 * kHalfBytes;      // 32 KB: K + V
+
+// Per-lane byte offsets of the HBM -> LDS loads of one step. Wave w fills K
+// and V segments 2w, 2w + 1 (1 KB = rows 4 seg .. 4 seg + 3 of the half);
+// lane l loads row 4 seg + l / 16, LDS chunk l % 16, which holds logical
+// chunk (l % 16) ^ (row & 15) of K and (l % 16) ^ 4 (row & 3) of V. `skip`
+// offsets re-read rows l / 16 instead (for segments wholly past the valid
+// count; what they write is never used).
+struct HDma {
+  uint32_t k[2], v[2], k_skip[2], v_skip[2];
+};
+
+__device__ __forceinline__ HDma hdma_offsets(int64_t ks, int64_t vs, int wave, int lane) {
+  HDma d;
+  const int lr = lane >> 4, pc = lane & 15;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    sacc[0][e] = 0.f;
-    sacc[1][e] = 0.f;
+  for (int u = 0; u < 2; ++u) {
+    const int row = 4 * (2 * wave + u) + lr;
+    const int kc = (pc ^ (row & 15)) << 3, vc = (pc ^ ((row & 3) << 2)) << 3;
+    d.k[u] = (uint32_t)((row * ks + kc) * 2);
+    d.v[u] = (uint32_t)((row * vs + vc) * 2);
+    d.k_skip[u] = (uint32_t)((lr * ks + kc) * 2);
+    d.v_skip[u] = (uint32_t)((lr * vs + vc) * 2);
   }
-  {
-    // row 64 kh + 32 t2 + li, logical chunk 2 s + hi at (2 s + hi) ^ (li & 15)
-    const int x = (hi ^ (li & 15)) << 4;
-    const lds_u8* r0 = kb + (64 * kh + li) * 256;
+  return d;
+}
+
+// One 16-byte-per-lane HBM -> LDS load (global_load_lds_dwordx4): lane l
+// reads 16 bytes at base + voff and writes them to LDS at dst + 16 l. It is
+// issued as inline assembly so that the compiler's wait-count tracking does
+// not see an LDS store behind it: that tracking merges conservatively at the
+// loop head and would make the first fragment read of a step wait for every
+// load in flight. The pipeline's explicit vmcnt waits order these loads;
+// untracked loads only ever make the compiler's own vmcnt waits stricter.
+// M0 (the LDS destination) is written inside the same statement, right
+// before its use; nothing else in these kernels uses M0 (the compiler
+// reports m0 as reserved in the clobber list and may not preserve it, which
+// is why no value in it may live across the statement).
+__device__ __forceinline__ void dma16(const char* base, uint32_t voff, const lds_u8* dst) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)dst;
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(base), "s"(m0)
+      : "memory", "m0");
+}
+
+// Issues the loads of the step at key row row0 (64 rows, the first vch >= 1
+// of them valid) into `slot`. CLAMP (the dense path's last tile, whose rows past the
+// valid count may lie past the end of k / v): every lane reads a row below
+// vch instead.
+template <bool CLAMP>
+__device__ __forceinline__ void issue_step(const uint16_t* kbase, const uint16_t* vbase,
+                                           const FwdParams& p, const HDma& d, int64_t row0,
+                                           int vch, int wave, int lane, lds_u8* slot) {
+  const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
+  const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int off = x ^ (s << 5);
-      const u32x4 a0 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(r0 + off);
-      const u32x4 a1 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(r0 + 32 * 256 + off);
-      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a0), w.qf[s], sacc[0], 0, 0, 0);
-      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a1), w.qf[s], sacc[1], 0, 0, 0);
+  for (int u = 0; u < 2; ++u) {
+    const int seg = 2 * wave + u;
+    const bool live = 4 * seg < vch;
+    uint32_t ko, vo;
+    if (CLAMP) {
+      const int lr = lane >> 4, pc = lane & 15, row = 4 * seg + lr;
+      const int src = min(live ? row : lr, vch - 1);
+      ko = (uint32_t)((src * p.ks + ((pc ^ (row & 15)) << 3)) * 2);
+      vo = (uint32_t)((src * p.vs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
+    } else {
+      ko = live ? d.k[u] : d.k_skip[u];
+      vo = live ? d.v[u] : d.v_skip[u];
     }
+    dma16(kb, ko, slot + seg * 1024);
+    dma16(vb, vo, slot + kHalfBytes + seg * 1024);
   }
-  // Register e of sub-tile t2 is key 64 kh + 32 t2 + 8 (e / 4) + 4 hi + e % 4.
-  if (vc < kTile) {
+}
+
+// Per-lane LDS offsets of the fragment reads inside a slot.
+struct HFrag {
+  uint32_t k[8];  // K row 32 kh + li, logical chunk 2k + hi
+  uint32_t v[4];  // V^T fragment base per dt (V region included)
+};
+
+__device__ __forceinline__ HFrag hfrag_offsets(int kh, int lane) {
+  HFrag f;
+  const int li = lane & 31, hi = lane >> 5;
+  const uint32_t krow = (32 * kh + li) * 256, x = (hi ^ (li & 15)) << 4;
 #pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2)
+  for (int k = 0; k < 8; ++k) f.k[k] = krow + (x ^ (k << 5));
+  // V^T of lane (16-lane group g = (hi, dh), i): transposed reads of rows
+  // 16 sg + 4 hi + i / 4 (+ 8), head-dims 32 dt + 16 dh + 4 (i % 4) .. + 3,
+  // sg = 2 kh + kk the 16-key group.
+  const int i16 = lane & 15, q4 = i16 >> 2, dh = (lane >> 4) & 1;
+  const uint32_t vb =
+      (4 * hi + q4) * 256 + (((2 * dh + ((i16 >> 1) & 1)) << 4) | (q4 << 6)) + (i16 & 1) * 8;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = 64 * kh + 32 * t2 + 8 * (e >> 2) + 4 * hi + (e & 3);
-        if (key >= vc) sacc[t2][e] = -INFINITY;
-      }
+  for (int dt = 0; dt < 4; ++dt) f.v[dt] = kHalfBytes + 2 * kh * 16 * 256 + (vb ^ (dt << 6));
+  return f;
+}
+
+// One step for this wave's 32 rows and 32 keys from `slot`; keys at or past
+// vch (of the half) are masked.
+__device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float c, int vch,
+                                      int kh, int hi, WaveState& w) {
+  u32x4 kf[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    kf[k] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(slot + f.k[k]);
+  f32x16 s;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) s[e] = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[k]), w.qf[k], s, 0, 0, 0);
+  // Register e holds key 32 kh + 8 (e / 4) + 4 hi + e % 4 of the half.
+  if (vch < 32 * (kh + 1)) {
+    const int lim = vch - 32 * kh - 4 * hi;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (8 * (e >> 2) + (e & 3) >= lim) s[e] = -INFINITY;
   }
-  // Online softmax in the log2 domain: p = exp2(s * c - m). The reference max
-  // m rises only when a row's max passes it by more than kRescaleSlack (p then
-  // stays <= 2^kRescaleSlack, exact in fp32 and bf16), so the O rescale is
-  // skipped for most blocks; numerator and denominator share m.
+  // Online softmax step in the log2 domain: p = exp2(s * c - m). The
+  // reference max m rises only when the step's row max passes it by more
+  // than kRescaleSlack (p then stays <= 2^kRescaleSlack, exact in fp32 and
+  // bf16), so the O rescale is skipped for most steps; numerator and
+  // denominator share m.
   float mloc = -INFINITY;
 #pragma unroll
-  for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sacc[t2][e]);
-  mloc = half_swap_max(mloc) * p.scale_log2;
+  for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
+  mloc = half_swap_max(mloc) * c;
   const float m_new = mloc > w.m_run + kRescaleSlack ? mloc : w.m_run;
-  const float m_use = m_new == -INFINITY ? 0.f : m_new;
-  const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_use);
+  const float mu = m_new == -INFINITY ? 0.f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(w.m_run - mu);
   w.m_run = m_new;
-  float lsum = 0.f;
-  u32x4 pk[2][2];
+  float ps[16];
 #pragma unroll
-  for (int t2 = 0; t2 < 2; ++t2)
+  for (int e = 0; e < 16; ++e) ps[e] = __builtin_amdgcn_exp2f(fmaf(s[e], c, -mu));
+  float l4[4];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+  for (int g = 0; g < 4; ++g) l4[g] = (ps[4 * g] + ps[4 * g + 1]) + (ps[4 * g + 2] + ps[4 * g + 3]);
+  w.l_run = fmaf(w.l_run, alpha, (l4[0] + l4[1]) + (l4[2] + l4[3]));
+  u32x4 pk[2];
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const float a = __builtin_amdgcn_exp2f(fmaf(sacc[t2][8 * kk + 2 * m], p.scale_log2, -m_use));
-        const float b = __builtin_amdgcn_exp2f(fmaf(sacc[t2][8 * kk + 2 * m + 1], p.scale_log2, -m_use));
-        lsum += a + b;
-        pk[t2][kk][m] = pack_bf16x2(a, b);
-      }
-  w.l_run = w.l_run * alpha + lsum;
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) pk[kk][m] = pack_bf16x2(ps[8 * kk + 2 * m], ps[8 * kk + 2 * m + 1]);
   if (__any(alpha != 1.f)) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) w.o[dt][e] *= alpha;
   }
-  // O^T += V^T P^T over the wave's four 16-key groups. Fragment of lane
-  // (16-lane group g = (hi, dh), i): two transposed reads of rows
-  // 16 s + 4 hi + i / 4 (+ 8), head-dims 32 dt + 16 dh + 4 (i % 4) .. + 3.
-  const int i16 = lane & 15, q4 = i16 >> 2, dh = (lane >> 4) & 1;
-  const int vbase = (4 * hi + q4) * 256 + (((2 * dh + ((i16 >> 1) & 1)) << 4) | (q4 << 6)) +
-                    (i16 & 1) * 8;
 #pragma unroll
-  for (int t2 = 0; t2 < 2; ++t2)
+  for (int kk = 0; kk < 2; ++kk) {
+    const lds_u8* vs = slot + kk * 16 * 256;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int s = 4 * kh + 2 * t2 + kk;
-      const bf16x8 b = as_bf16x8(pk[t2][kk]);
-      const lds_u8* vs = vb + s * 16 * 256;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const int off = vbase ^ (dt << 6);
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + off));
-        const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + 8 * 256 + off));
-        typedef short i16x8 __attribute__((ext_vector_type(8)));
-        const i16x8 a = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
-        w.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, w.o[dt],
-                                                         0, 0, 0);
-      }
+    for (int dt = 0; dt < 4; ++dt) {
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + f.v[dt]));
+      const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + 8 * 256 + f.v[dt]));
+      const bf16x8 a =
+          __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
+      w.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pk[kk]), w.o[dt], 0, 0, 0);
     }
+  }
 }
 
+// vmcnt waits as s_waitcnt immediates (gfx9 encoding: vmcnt low bits [3:0],
+// expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
+#define VEDA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+
 template <bool DENSE>
-__global__ void __launch_bounds__(kThreads) fwd_kernel(FwdParams p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t stage0[kStageBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t stage1[kStageBytes];
-  __shared__ int32_t walk_j[kMaxBlocks];
-  __shared__ int32_t walk_vc[kMaxBlocks];
-  lds_u8* st0 = (lds_u8*)stage0;
-  lds_u8* st1 = (lds_u8*)stage1;
+__global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t slot0[kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t slot1[kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t slot2[kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t slot3[kSlotBytes];
+  __shared__ int32_t step_list[2 * kMaxBlocks];
+  __shared__ int32_t step_total;
+  lds_u8* sl0 = (lds_u8*)slot0;
+  lds_u8* sl1 = (lds_u8*)slot1;
+  lds_u8* sl2 = (lds_u8*)slot2;
+  lds_u8* sl3 = (lds_u8*)slot3;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int qg = wave & 3, kh = wave >> 2;
   const int li = lane & 31, hi = lane >> 5;
   const int64_t item = blockIdx.x;
@@ -235,46 +309,73 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(FwdParams p) {
   const int64_t r = item % p.n_q_tiles;
   const int64_t qrow = r * kTile + 32 * qg + li;
 
-  int nf, nb;
+  // Zero the ring (stale rows are multiplied by p = 0 only; see above).
+  for (int i = tid; i < kSlotBytes / 16; i += kThreads) {
+    reinterpret_cast<u32x4*>(slot0)[i] = u32x4{0, 0, 0, 0};
+    reinterpret_cast<u32x4*>(slot1)[i] = u32x4{0, 0, 0, 0};
+    reinterpret_cast<u32x4*>(slot2)[i] = u32x4{0, 0, 0, 0};
+    reinterpret_cast<u32x4*>(slot3)[i] = u32x4{0, 0, 0, 0};
+  }
+
+  // Step list: one word per step, (first key row << 7) | valid keys of the
+  // step (0..64). Blocks in walk order (full list first): a full key tile
+  // is two steps; a partial tile is one step for its first half, plus one
+  // for its second half when more than 64 keys are valid -- those second
+  // halves go after all first halves, in walk order (ranked by a ballot,
+  // so the list, and with it the summation order, is deterministic). An
+  // entry outside [0, n_k_tiles) keeps no key (steps with 0 valid keys,
+  // loading tile 0). The dense path needs no list: step u is rows
+  // 64 u .. 64 u + 63.
+  int n_steps;
   if (DENSE) {
-    nf = 0;
-    nb = (int)((p.used + kTile - 1) / kTile);
+    const int64_t nsteps = (p.used + kHalf - 1) / kHalf;
+    n_steps = (int)nsteps;
   } else {
     const int64_t li_ = head * p.n_q_tiles + r;
     const int ld = (int)p.list_ld;
-    nf = min(max(p.full_cnt[li_], 0), ld);
-    nb = min(nf + min(max(p.part_cnt[li_], 0), ld), kMaxBlocks);
-    // The block walk -- key tile and valid key count of every step, full
-    // list first -- goes to LDS once, so the loop reads no list or count
-    // from global memory (a vector load behind the in-flight K / V loads
-    // would make its wait a wait for them). An entry outside [0, n_k_tiles)
-    // keeps no key.
+    const int nf = min(max(p.full_cnt[li_], 0), min(ld, kMaxBlocks));
+    const int np = min(max(p.part_cnt[li_], 0), min(ld, kMaxBlocks - nf));
     const int32_t* fl = p.full_idx + li_ * p.list_ld;
     const int32_t* pl = p.part_idx + li_ * p.list_ld;
-    for (int i = tid; i < nb; i += kThreads) {
-      int64_t j = i < nf ? fl[i] : pl[i - nf];
-      int vc;
-      if (j < 0 || j >= p.n_k_tiles) {
-        j = 0;
-        vc = 0;
-      } else {
-        vc = i < nf ? kTile : p.valid_count[j];
+    for (int i = tid; i < nf; i += kThreads) {
+      const int32_t j = fl[i];
+      const bool ok = j >= 0 && j < p.n_k_tiles;
+      const int32_t row0 = ok ? j * kTile : 0;
+      step_list[2 * i] = (row0 << 7) | (ok ? kHalf : 0);
+      step_list[2 * i + 1] = ((row0 + kHalf) << 7) | (ok ? kHalf : 0);
+    }
+    if (wave == 0) {
+      int h1 = 0;
+      for (int i0 = 0; i0 < np; i0 += 64) {
+        const int i = i0 + lane;
+        int32_t row0 = 0;
+        int vc = 0;
+        if (i < np) {
+          const int32_t j = pl[i];
+          if (j >= 0 && j < p.n_k_tiles) {
+            row0 = j * kTile;
+            vc = p.valid_count[j];
+          }
+          step_list[2 * nf + i] = (row0 << 7) | min(vc, kHalf);
+        }
+        const bool two = i < np && vc > kHalf;
+        const uint64_t bal = __ballot(two);
+        const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+        if (two) step_list[2 * nf + np + h1 + rank] = ((row0 + kHalf) << 7) | (vc - kHalf);
+        h1 += __builtin_popcountll(bal);
       }
-      walk_j[i] = (int32_t)j;
-      walk_vc[i] = vc;
+      if (lane == 0) step_total = 2 * nf + np + h1;
     }
   }
 
   WaveState w;
-  // Q^T fragments: lane (li, hi) holds q[qrow, 16 s + 8 hi + 0..7].
-  const bool q_ok = DENSE ? (qrow < p.used) : true;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
+    const bool q_ok = DENSE ? (qrow < p.used) : true;
     u32x4 v = q_ok ? ld16(p.q + qrow * p.qs + head * p.qh + 16 * s + 8 * hi) : u32x4{0, 0, 0, 0};
     w.qf[s] = as_bf16x8(v);
   }
-  // Consume the Q loads here: otherwise the wait-count pass carries them into
-  // the loop and waits on the in-flight K/V loads before every MFMA.
 #pragma unroll
   for (int s = 0; s < 8; ++s) asm volatile("" : : "v"(w.qf[s]));
 #pragma unroll
@@ -283,43 +384,88 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(FwdParams p) {
     for (int e = 0; e < 16; ++e) w.o[dt][e] = 0.f;
   w.m_run = -INFINITY;
   w.l_run = 0.f;
-  __syncthreads();  // walk ready
+  __syncthreads();  // step list, step count and zeroed ring ready
+  if (!DENSE) n_steps = __builtin_amdgcn_readfirstlane(step_total);
 
-  auto step_block = [&](int t) -> int64_t {
-    return DENSE ? t : __builtin_amdgcn_readfirstlane(walk_j[t]);
+  // (first key row, valid keys) of step u
+  auto step_row = [&](int u) -> int64_t {
+    return DENSE ? (int64_t)u * kHalf : (int64_t)(__builtin_amdgcn_readfirstlane(step_list[u]) >> 7);
   };
-  auto step_count = [&](int t) -> int {
+  auto step_vch = [&](int u) -> int {
     if (DENSE) {
-      const int64_t rem = p.used - (int64_t)t * kTile;
-      return rem < kTile ? (int)rem : kTile;
+      const int64_t rem = p.used - (int64_t)u * kHalf;
+      return rem < kHalf ? (int)rem : kHalf;
     }
-    return __builtin_amdgcn_readfirstlane(walk_vc[t]);
+    return __builtin_amdgcn_readfirstlane(step_list[u]) & 127;
   };
-  if (nb > 0) issue_stage(p, head, step_block(0), wave, lane, st0);
-  for (int t = 0; t < nb; t += 2) {
-    // even step: compute stage 0 while stage 1 fills
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t + 1 < nb) issue_stage(p, head, step_block(t + 1), wave, lane, st1);
-    attend_block(p, st0, step_count(t), kh, li, hi, lane, w);
-    if (t + 1 >= nb) break;
-    // odd step: compute stage 1 while stage 0 fills
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t + 2 < nb) issue_stage(p, head, step_block(t + 2), wave, lane, st0);
-    attend_block(p, st1, step_count(t + 1), kh, li, hi, lane, w);
+  const uint16_t* kbase = p.k + head * p.kh;
+  const uint16_t* vbase = p.v + head * p.vh;
+  const float c = p.scale_log2;
+  const HDma dma = hdma_offsets(p.ks, p.vs, wave, lane);
+  const HFrag frag = hfrag_offsets(kh, lane);
+
+  auto load_step = [&](int u, lds_u8* slot) {
+    const int vch = step_vch(u);
+    // a step with no valid key (an empty or out-of-range tile) loads the
+    // tile's first rows, which exist; its keys are all masked
+    if (DENSE && vch < kHalf)
+      issue_step<true>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
+    else
+      issue_step<false>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
+  };
+  // Prologue: steps 0, 1, 2 into slots 0, 1, 2.
+  if (n_steps > 0) load_step(0, sl0);
+  if (n_steps > 1) load_step(1, sl1);
+  if (n_steps > 2) load_step(2, sl2);
+  // Step u: wait for its own loads (every step is 4 loads per wave; the
+  // loads of steps u+1, u+2 may stay in flight), barrier, refill the slot
+  // step u-1 used with step u+3, compute step u.
+  // The barrier is a bare s_barrier: __syncthreads() would also fence
+  // memory, i.e. wait for every load in flight. LDS is coherent inside the
+  // workgroup, the step's DMA is complete in every wave once each has waited
+  // for its own loads, and every fragment read of the previous step has been
+  // consumed by an MFMA before its wave reaches the barrier.
+  auto wait_step = [&](int u) {
+    if (u + 2 < n_steps) VEDA_WAIT_VM(8);
+    else if (u + 1 < n_steps) VEDA_WAIT_VM(4);
+    else VEDA_WAIT_VM(0);
+    __builtin_amdgcn_s_barrier();
+  };
+  // A wave whose 32 keys of the step are all padding skips the step: all
+  // its scores would be -inf, which leaves m, l and O unchanged.
+  auto compute_step = [&](int u, const lds_u8* slot) {
+    const int vch = step_vch(u);
+    if (vch > 32 * kh) hstep(slot, frag, c, vch, kh, hi, w);
+  };
+  for (int u = 0; u < n_steps; u += 4) {
+    wait_step(u);
+    if (u + 3 < n_steps) load_step(u + 3, sl3);
+    compute_step(u, sl0);
+    if (u + 1 >= n_steps) break;
+    wait_step(u + 1);
+    if (u + 4 < n_steps) load_step(u + 4, sl0);
+    compute_step(u + 1, sl1);
+    if (u + 2 >= n_steps) break;
+    wait_step(u + 2);
+    if (u + 5 < n_steps) load_step(u + 5, sl1);
+    compute_step(u + 2, sl2);
+    if (u + 3 >= n_steps) break;
+    wait_step(u + 3);
+    if (u + 6 < n_steps) load_step(u + 6, sl2);
+    compute_step(u + 3, sl3);
   }
-  __syncthreads();  // every wave is done reading both stages
+  __syncthreads();  // every wave is done reading the ring
 
   // Merge the two key halves: kh = 1 hands (m, l, O) to kh = 0 through LDS.
   w.l_run = half_swap_sum(w.l_run);
-  float* red = reinterpret_cast<float*>(stage0);  // [qg][64 regs][64 lanes] = 64 KB
-  float* ml = reinterpret_cast<float*>(stage1);   // [qg][2][32]
+  // [qg & 1][64 regs][64 lanes] in slot 0 (qg < 2) or slot 1 (qg >= 2)
+  float* red = reinterpret_cast<float*>(qg < 2 ? slot0 : slot1) + (qg & 1) * 64 * 64;
+  float* ml = reinterpret_cast<float*>(slot2);  // [qg][m | l][32]
   if (kh == 1) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) red[(qg * 64 + dt * 16 + e) * 64 + lane] = w.o[dt][e];
+      for (int e = 0; e < 16; ++e) red[(dt * 16 + e) * 64 + lane] = w.o[dt][e];
     if (hi == 0) {
       ml[qg * 64 + li] = w.m_run;
       ml[qg * 64 + 32 + li] = w.l_run;
@@ -344,7 +490,7 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(FwdParams p) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int e = 4 * g + rr;
-        const float o1 = red[(qg * 64 + dt * 16 + e) * 64 + lane];
+        const float o1 = red[(dt * 16 + e) * 64 + lane];
         v4[rr] = (w.o[dt][e] * a0 + o1 * a1) * inv;
       }
       const int d = 32 * dt + 8 * g + 4 * hi;
@@ -411,7 +557,7 @@ extern "C" int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t 
   p.os = o_stride_s; p.oh = o_stride_h;
   p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  fwd_kernel<false><<<(unsigned)items, kThreads, 0, s>>>(p);
+  hfwd_kernel<false><<<(unsigned)items, kThreads, 0, s>>>(p);
   return check_launch("veda_block_sparse_fwd");
 }
 
@@ -449,6 +595,6 @@ extern "C" int veda_dense_fwd(const void* q, int64_t q_stride_s, int64_t q_strid
   p.os = o_stride_s; p.oh = o_stride_h;
   p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  fwd_kernel<true><<<(unsigned)items, kThreads, 0, s>>>(p);
+  hfwd_kernel<true><<<(unsigned)items, kThreads, 0, s>>>(p);
   return check_launch("veda_dense_fwd");
 }

@@ -29,13 +29,18 @@ FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
          f'-I{ROOT / "include"}']
 
 
+# Per-source extra flags. attention.hip: MFMA results in VGPRs (the softmax
+# reads every score; the default AGPR form costs a copy per score).
+EXTRA = {'attention.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
+
+
 def sources() -> list[pathlib.Path]:
     return sorted(HERE.glob('*.hip'))
 
 
 def _compile(src: pathlib.Path) -> pathlib.Path:
     obj = BUILD_DIR / (src.stem + '.o')
-    cmd = [HIPCC, *FLAGS, '-c', str(src), '-o', str(obj)]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src.name, []), '-c', str(src), '-o', str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f'hipcc failed on {src.name}:\n{proc.stderr}')
