@@ -135,6 +135,128 @@ def _traffic() -> float | None:
     return None
 
 
+def _median_ms(fn, reps: int = 5) -> float:
+    fn()
+    torch.cuda.synchronize()
+    t = sorted(_events_ms(fn, reps))
+    return t[len(t) // 2]
+
+
+def _hbm(ms: float, nbytes: float) -> dict:
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {'ms': round(ms, 4), 'bytes': nbytes, 'bound': 'hbm', 'achieved': round(gbs, 1),
+            'unit': 'GB/s', 'peak': PEAK_HBM_GBS, 'frac': round(gbs / PEAK_HBM_GBS, 4)}
+
+
+def _mfma(ms: float, flop: float) -> dict:
+    tf = flop / (ms * 1e-3) / 1e12
+    return {'ms': round(ms, 4), 'flop': flop, 'bound': 'mfma', 'achieved': round(tf, 1),
+            'unit': 'TFLOP/s', 'peak': PEAK_BF16_TFLOPS, 'frac': round(tf / PEAK_BF16_TFLOPS, 4)}
+
+
+def suite(reps: int = 5) -> dict:
+    """Every kernel of the path at its BASELINE configuration, each against
+    its own roofline (HBM-bound kernels: algorithmic bytes; MFMA-bound:
+    algorithmic FLOP; selection and predictor are small and reported as time).
+    Synthetic seeded inputs, resident in HBM before timing."""
+    from miowtion_amd import attention as pa, kernels, mask as pm, plan as pplan
+    from miowtion_amd import predictor as pp, tiling as pt
+    res = {}
+    # ---- C2: 57,720 tokens x 48 heads, (1,8,16) tiles
+    _log('suite: C2')
+    c = build_case()
+    lay, q, v = c['lay'], c['q'], c['v']
+    n, N, used = lay.n_tiles, lay.num_slots, c['used']
+    row = HEADS * D * 2  # bytes of one [H, D] bf16 row
+    feats = HEADS * n * 3 * D * 4
+    ms = _median_ms(lambda: kernels.gather_and_pool(q, lay, None), reps)
+    res['gather_pool_q_c2'] = _hbm(ms, used * row + N * row + feats)
+    ms = _median_ms(lambda: kernels.gather_tiles(v, lay, None), reps)
+    res['gather_v_c2'] = _hbm(ms, used * row + N * row)
+    outbuf = torch.zeros(c['seq_len'] + 1, HEADS, D, dtype=torch.bfloat16, device='cuda')
+    ms = _median_ms(lambda: kernels.scatter_tiles_(outbuf, c['qt'], lay, None), reps)
+    res['scatter_c2'] = _hbm(ms, 2 * used * row)
+    blocks = pm.column_blocks(lay, pm.Budget(ratio=RATIO))
+    ms = _median_ms(lambda: pm.select_video_blocks(c['scores'], lay, blocks), reps)
+    res['select_topk_c2'] = {'ms': round(ms, 4), 'bound': 'small (reported, not rooflined)'}
+    ms = _median_ms(lambda: kernels.index_lists(c['mask'], lay), reps)
+    res['index_lists_c2'] = _hbm(ms, HEADS * n * n * (1 + 2 * 4) + 2 * HEADS * n * 4)
+    pred = pp.LayerPredictor.random(HEADS, D, std=0.02, generator=torch.Generator().manual_seed(1),
+                                    device='cuda', fp8=True)
+    _, fq = kernels.gather_and_pool(q, lay, None)
+    _, fk = kernels.gather_and_pool(c['k'], lay, None)
+    heads = torch.arange(HEADS, device='cuda')
+    ms = _median_ms(lambda: pred(fq, fk, heads), reps)
+    pflop = 2 * 2.0 * n * 3 * D * D * HEADS + 2.0 * n * n * D * HEADS
+    res['predictor_c2'] = {'ms': round(ms, 4), 'flop': pflop,
+                           'tflops_fp32': round(pflop / (ms * 1e-3) / 1e12, 2),
+                           'bound': 'small (fp32 GEMMs, reported, not rooflined)'}
+    kept = int(c['mask'].sum())
+    ms = _median_ms(lambda: kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'],
+                                                                 c['lists'], lay), reps)
+    res['sparse_fwd_c2'] = _mfma(ms, 4.0 * 128 * 128 * D * kept)
+    ms = _median_ms(lambda: kernels.dense_attention(q, c['k'], v, used, return_lse=True), 3)
+    res['dense_fwd_lse_c2'] = _mfma(ms, 4.0 * used * used * HEADS * D)
+    del c, outbuf, fq, fk
+    torch.cuda.empty_cache()
+
+    # ---- C3: 9:16 grid, per-head shape (1,8,16) or (4,4,8), keep 0.2, full layer
+    _log('suite: C3')
+    grid3 = (37, 52, 30)
+    used3 = grid3[0] * grid3[1] * grid3[2]
+    seq3 = -(-used3 // 64) * 64
+    g = torch.Generator(device='cuda').manual_seed(3)
+    q3, k3, v3 = (torch.randn(seq3, HEADS, D, generator=g, device='cuda').to(torch.bfloat16)
+                  for _ in range(3))
+    layout3 = pa.PackedLayout((pa.VideoSpan(0, grid3),), used3, seq3)
+    clip3 = pa.ClipTiling(layout3, pa.VedaConfig(target_budget=pm.Budget(ratio=0.2)), 'cuda')
+    choice = torch.randint(0, 2, (HEADS,), generator=torch.Generator().manual_seed(3))
+    shapes = [pt.TileShape(1, 8, 16), pt.TileShape(4, 4, 8)]
+    plan3 = pplan.TilePlan('9x16_t37_c3', grid3, shapes, [choice.tolist()])
+    pred3 = pp.TileScorePredictor([pp.LayerPredictor.random(
+        HEADS, D, std=0.02, generator=torch.Generator().manual_seed(4), device='cuda', fp8=True)])
+    student3 = pa.SparseStudent(clip3, plan3, pred3)
+    ms = _median_ms(lambda: student3(q3, k3, v3, 0), 3)
+    res['veda_layer_c3'] = {'ms': round(ms, 4), 'groups': [int((choice == i).sum()) for i in (0, 1)],
+                            'bound': 'whole layer (gather/pool, predictor, selection, lists, '
+                                     'sparse forward, scatter), reported as time'}
+    del q3, k3, v3, student3, clip3
+    torch.cuda.empty_cache()
+
+    # ---- C5: 2,048 global rows + 102x30x52 video, keep 0.05
+    _log('suite: C5')
+    grid5 = (102, 30, 52)
+    start5 = 2048
+    used5 = start5 + grid5[0] * grid5[1] * grid5[2]
+    seq5 = -(-used5 // 64) * 64
+    lay5 = pt.build_tile_layout([pt.TiledSpan(start5, grid5, pt.TileShape(1, 8, 16))], used5,
+                                seq5, 'cuda')
+    g = torch.Generator(device='cuda').manual_seed(5)
+    q5, k5, v5 = (torch.randn(seq5, HEADS, D, generator=g, device='cuda').to(torch.bfloat16)
+                  for _ in range(3))
+    for t in (q5, k5, v5):
+        t[used5:] = 0
+    ms = _median_ms(lambda: kernels.dense_attention(q5, k5, v5, used5, return_lse=True), 3)
+    res['dense_fwd_lse_c5'] = _mfma(ms, 4.0 * used5 * used5 * HEADS * D)
+    _, lse5 = kernels.dense_attention(q5, k5, v5, used5, return_lse=True)
+    qt5, kt5, vt5 = (kernels.gather_tiles(t, lay5, None) for t in (q5, k5, v5))
+    lse_t = kernels.gather_lse(lse5, lay5, heads)
+    n5, nv5 = lay5.n_tiles, lay5.n_video_tiles
+    rows5 = torch.arange(nv5, device='cuda')
+    ms = _median_ms(lambda: kernels.teacher_heat(qt5, kt5, lse_t, lay5, rows5, 'sum'), 3)
+    res['heat_sum_c5'] = _mfma(ms, 2.0 * 128 * 128 * D * nv5 * n5 * HEADS)
+    heat = kernels.teacher_heat(qt5, kt5, lse_t, lay5, rows5, 'sum')
+    blocks5 = pm.column_blocks(lay5, pm.Budget(ratio=0.05))
+    sel5 = pm.select_video_blocks(heat[:, :, :nv5], lay5, blocks5, rows5)
+    mask5 = pm.dense_block_mask(sel5, lay5)
+    lists5 = kernels.index_lists(mask5, lay5)
+    kept5 = int(mask5.sum())
+    ms = _median_ms(lambda: kernels.block_sparse_attention_lists(qt5, kt5, vt5, lists5, lay5), 3)
+    res['sparse_fwd_c5'] = _mfma(ms, 4.0 * 128 * 128 * D * kept5)
+    res['sparse_fwd_c5']['kept_blocks'] = kept5
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -145,6 +267,9 @@ def main() -> int:
     ap.add_argument('--cpu-budget', type=float, default=20.0)
     ap.add_argument('--only-kernel', action='store_true',
                     help='time the sparse forward only (for rocprofv3 runs)')
+    ap.add_argument('--suite', action='store_true',
+                    help='time every kernel of the path at its BASELINE config against its '
+                         'roofline and print that JSON instead of the headline line')
     ap.add_argument('--copy-bytes', type=int, default=0,
                     help='first run 3 device-to-device copies of this many bytes: the known-size '
                          'reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings')
@@ -155,6 +280,9 @@ def main() -> int:
               'shares -- run with --gpus 1', file=sys.stderr)
         return 2
     from miowtion_amd import kernels, mask as pm
+    if args.suite:
+        print(json.dumps({'suite': suite(), 'gpu': torch.cuda.get_device_name(0)}), flush=True)
+        return 0
     if args.copy_bytes:
         n = args.copy_bytes // 4
         src = torch.ones(n, dtype=torch.float32, device='cuda')
