@@ -188,14 +188,18 @@ int veda_dense_fwd(const void* q, int64_t q_stride_s, int64_t q_stride_h,
  *   reduce 0 ('sum'): heat[h, r, j] = sum over real rows i of tile
  *     q_tiles[r] and real keys c of tile j of exp(q_i.k_c * scale - lse_i);
  *   reduce 1 ('max'): exp(max_i(bf16(max_c q_i.k_c) * scale - lse_i)).
- * Scores are fp32 (MFMA accumulation); padding rows/keys contribute nothing.
- * q, k: bf16 [N, H', D] with strides; lse: fp32 [N, H'] with strides;
- * heat: fp32 [n_heads, n_q, n_tiles] contiguous. head_dim: 128.
+ * The real rows of tile t are its first valid_count[t] slots (the tile
+ * layout's prefix rule, tiling.py:9-16); padding rows and keys contribute
+ * nothing; a q_tiles entry outside [0, n_tiles) gets a zero row. Scores are
+ * fp32 (MFMA accumulation).
+ * q, k: bf16 [n_tiles * 128, H', D] with strides; lse: fp32 [N, H'] with
+ * strides; valid_count: int32 [n_tiles]; heat: fp32 [n_heads, n_q, n_tiles]
+ * contiguous. head_dim: 128; n_tiles <= 2048.
  */
 int veda_block_heat(const void* q, int64_t q_stride_s, int64_t q_stride_h,
                     const void* k, int64_t k_stride_s, int64_t k_stride_h,
                     const float* lse, int64_t lse_stride_s,
-                    int64_t lse_stride_h, const int32_t* slot_valid,
+                    int64_t lse_stride_h, const int32_t* valid_count,
                     const int64_t* q_tiles, int64_t n_q, int64_t n_tiles,
                     int64_t n_heads, int64_t head_dim, int reduce, float scale,
                     float* heat, void* stream);

@@ -29,6 +29,7 @@
 // The pipeline over the kept blocks is described at the half-block section.
 
 #include "veda_common.h"
+#include "veda_pipeline.h"
 
 namespace veda {
 namespace {
@@ -40,10 +41,6 @@ constexpr int kMaxBlocks = 2048;                 // key tiles per row (FA4's cap
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleSlack = 8.f;             // log2 units
 
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-typedef __attribute__((address_space(3))) void lds_void;
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 struct FwdParams {
   const uint16_t* q;
@@ -67,22 +64,6 @@ struct FwdParams {
   int64_t lse_sh, lse_ss;
 };
 
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-__device__ __forceinline__ u32x4 ld16(const uint16_t* p) {
-  return *reinterpret_cast<const u32x4*>(p);
-}
-
-// max / sum with the lane 32 positions away (v_permlane32_swap leaves {own,
-// partner} in the two results of every lane, in either order).
-__device__ __forceinline__ float half_swap_max(float v) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float half_swap_sum(float v) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
 // Per-wave state: Q^T fragments of the wave's 32 rows (lane (li, hi) holds
 // q[row 32 qg + li, 16 s + 8 hi .. + 7]), the O^T accumulators
@@ -115,8 +96,6 @@ struct WaveState {
 // O^T += V^T P^T (8 MFMAs); a wave whose 32 keys are all padding skips the
 // step. The two key halves merge at the end.
 
-constexpr int kHalf = 64;                       // keys per step
-constexpr int kHalfBytes = kHalf * kD * 2;      // 16 KB: K or V of a step
 constexpr int kSlotBytes = 2 * kHalfBytes;      // 32 KB: K + V
 
 // Per-lane byte offsets of the HBM -> LDS loads of one step. Wave w fills K
@@ -144,27 +123,6 @@ __device__ __forceinline__ HDma hdma_offsets(int64_t ks, int64_t vs, int wave, i
   return d;
 }
 
-// One 16-byte-per-lane HBM -> LDS load (global_load_lds_dwordx4): lane l
-// reads 16 bytes at base + voff and writes them to LDS at dst + 16 l. It is
-// issued as inline assembly so that the compiler's wait-count tracking does
-// not see an LDS store behind it: that tracking merges conservatively at the
-// loop head and would make the first fragment read of a step wait for every
-// load in flight. The pipeline's explicit vmcnt waits order these loads;
-// untracked loads only ever make the compiler's own vmcnt waits stricter.
-// M0 (the LDS destination) is written inside the same statement, right
-// before its use; nothing else in these kernels uses M0 (the compiler
-// reports m0 as reserved in the clobber list and may not preserve it, which
-// is why no value in it may live across the statement).
-__device__ __forceinline__ void dma16(const char* base, uint32_t voff, const lds_u8* dst) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)dst;
-  asm volatile(
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, %1"
-      :
-      : "v"(voff), "s"(base), "s"(m0)
-      : "memory", "m0");
-}
 
 // Issues the loads of the step at key row row0 (64 rows, the first vch >= 1
 // of them valid) into `slot`. CLAMP (the dense path's last tile, whose rows past the
@@ -284,9 +242,6 @@ __device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float 
   }
 }
 
-// vmcnt waits as s_waitcnt immediates (gfx9 encoding: vmcnt low bits [3:0],
-// expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
-#define VEDA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
 
 template <bool DENSE>
 __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {

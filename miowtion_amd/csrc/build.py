@@ -29,9 +29,11 @@ FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
          f'-I{ROOT / "include"}']
 
 
-# Per-source extra flags. attention.hip: MFMA results in VGPRs (the softmax
-# reads every score; the default AGPR form costs a copy per score).
-EXTRA = {'attention.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
+# Per-source extra flags. attention.hip, heat.hip: MFMA results in VGPRs
+# (the softmax / heat reads every score; the default AGPR form costs a copy
+# per score).
+EXTRA = {'attention.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form'],
+         'heat.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
 
 
 def sources() -> list[pathlib.Path]:

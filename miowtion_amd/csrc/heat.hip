@@ -1,23 +1,28 @@
 // Teacher block heat for gfx950: per (head, query tile, key tile) the block's
 // softmax mass ('sum') or peak probability ('max') from the dense LSE.
 //
-// Workgroup = (head, query tile, run of 16 key tiles), 4 waves; wave w owns
-// query rows 32w .. 32w+31 of the tile and keeps them in registers as the
-// B operand of S^T = K Q^T (v_mfma_f32_32x32x16_bf16), so each lane holds one
-// query row and 64 of the 128 keys of a block. K tiles are double-buffered
-// in LDS (16-byte XOR swizzle, as in the attention kernel) together with a
-// 128-bit key-validity mask; the next tile is loaded while the current one
-// is reduced. Only one fp32 value per block leaves the workgroup.
+// Workgroup = (head, query tile): 8 waves walk every key tile of the head
+// through the same pipeline as the attention kernel, with K only: 64-key
+// steps in a 4-slot LDS ring (three steps in flight), padding rows (past a
+// tile's valid count) not fetched, an upper half with no valid key no step
+// at all. Wave w = (query group qg = w & 3: rows 32 qg .. + 31, key half
+// kh = w >> 2: keys 32 kh .. + 31 of every step) keeps its rows' Q^T in
+// registers as the B operand of S^T = K Q^T (v_mfma_f32_32x32x16_bf16), so
+// each lane holds one query row and 16 keys of a step. A step's contribution
+// is reduced over the wave (DPP and lane swaps, no LDS round trip) and added
+// (or max-ed) into the wave's own LDS slot for that key tile; the eight
+// waves' slots are combined in a fixed order at the end, so the result does
+// not depend on timing. Only one fp32 value per block leaves the workgroup.
 
 #include "veda_common.h"
+#include "veda_pipeline.h"
 
 namespace veda {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kHeatThreads = 256;
-constexpr int kTilesPerGroup = 16;
-constexpr int kKBytes = kTile * kD * 2;  // 32 KB
+constexpr int kHeatThreads = 512;
+constexpr int kMaxTiles = 2048;  // key tiles per layout (FA4's block-mask cap)
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct HeatParams {
@@ -26,135 +31,215 @@ struct HeatParams {
   int64_t qs, qh, ks, kh;
   const float* lse;
   int64_t ls, lh;
-  const int32_t* slot_valid;
+  const int32_t* valid_count;
   const int64_t* q_tiles;
-  int64_t n_q, n_tiles, n_heads, n_groups;
-  int reduce;  // 0 sum, 1 max
+  int64_t n_q, n_tiles, n_heads;
   float scale;
   float* heat;
 };
 
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+// Per-lane byte offsets of this wave's two 1 KB K segments of a step (rows
+// 4 seg + l / 16, LDS chunk l % 16 holding logical chunk (l % 16) ^ (row &
+// 15)) and of their redirect (rows l / 16) for segments wholly past the
+// valid count.
+struct KDma {
+  uint32_t k[2], skip[2];
+};
 
-__device__ __forceinline__ void load_k(const HeatParams& p, int64_t head, int64_t j, int tid,
-                                       u32x4 (&st)[8], int& valid) {
-  const int64_t row0 = j * kTile;
+__device__ __forceinline__ KDma kdma_offsets(int64_t ks, int wave, int lane) {
+  KDma d;
+  const int lr = lane >> 4, pc = lane & 15;
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int c = tid + 256 * u;
-    const int row = c >> 4, ch = c & 15;
-    st[u] = *reinterpret_cast<const u32x4*>(p.k + (row0 + row) * p.ks + head * p.kh + ch * 8);
+  for (int u = 0; u < 2; ++u) {
+    const int row = 4 * (2 * wave + u) + lr;
+    const int kc = (pc ^ (row & 15)) << 3;
+    d.k[u] = (uint32_t)((row * ks + kc) * 2);
+    d.skip[u] = (uint32_t)((lr * ks + kc) * 2);
   }
-  valid = tid < kTile ? p.slot_valid[row0 + tid] : 0;
+  return d;
 }
 
-__device__ __forceinline__ void store_k(uint8_t* buf, uint64_t* vmask, int tid,
-                                        const u32x4 (&st)[8], int valid) {
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int c = tid + 256 * u;
-    const int row = c >> 4, ch = c & 15;
-    *reinterpret_cast<u32x4*>(buf + row * 256 + ((ch ^ (row & 15)) << 4)) = st[u];
-  }
-  const uint64_t b = __ballot(valid != 0);
-  if (tid < kTile && (tid & 63) == 0) vmask[tid >> 6] = b;
-}
-
+template <int REDUCE>  // 0: sum, 1: max
 __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t kbuf[2][kKBytes];
-  __shared__ uint64_t vmask[2][2];
-  __shared__ float part[4][kTilesPerGroup];
+  __shared__ __attribute__((aligned(1024))) uint8_t kr0[kHalfBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t kr1[kHalfBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t kr2[kHalfBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t kr3[kHalfBytes];
+  __shared__ int32_t step_list[2 * kMaxTiles];
+  __shared__ float part[8][kMaxTiles];
+  __shared__ int32_t step_total;
+  lds_u8* K0 = (lds_u8*)kr0;
+  lds_u8* K1 = (lds_u8*)kr1;
+  lds_u8* K2 = (lds_u8*)kr2;
+  lds_u8* K3 = (lds_u8*)kr3;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int qg = wave & 3, kh = wave >> 2;
   const int li = lane & 31, hi = lane >> 5;
   const int64_t item = blockIdx.x;
-  const int64_t g = item % p.n_groups;
-  const int64_t hr = item / p.n_groups;
-  const int64_t r = hr % p.n_q;
-  const int64_t head = hr / p.n_q;
+  const int64_t head = item / p.n_q;
+  const int64_t r = item % p.n_q;
   const int64_t qt = p.q_tiles[r];
-  const int64_t j0 = g * kTilesPerGroup;
-  const int64_t j1 = j0 + kTilesPerGroup < p.n_tiles ? j0 + kTilesPerGroup : p.n_tiles;
-  const int nt = (int)(j1 - j0);
+  const int nt = (int)p.n_tiles;
+  float* heat_row = p.heat + (head * p.n_q + r) * p.n_tiles;
   if (qt < 0 || qt >= p.n_tiles) {  // not a query tile of this layout: no heat
-    if (tid < nt) p.heat[(head * p.n_q + r) * p.n_tiles + j0 + tid] = 0.f;
+    for (int j = tid; j < nt; j += kHeatThreads) heat_row[j] = 0.f;
     return;
   }
-  const int64_t qrow = qt * kTile + 32 * wave + li;
 
+  // Zero the ring (stale rows only ever meet masked keys), reset the
+  // partials, and build the step list: (key tile << 8) | (half << 7) | valid
+  // keys of the half; first halves of all tiles in tile order, then the
+  // second halves of tiles with more than 64 valid keys (ranked by a ballot).
+  for (int i = tid; i < kHalfBytes / 16; i += kHeatThreads) {
+    const u32x4 z = {0, 0, 0, 0};
+    reinterpret_cast<u32x4*>(kr0)[i] = z;
+    reinterpret_cast<u32x4*>(kr1)[i] = z;
+    reinterpret_cast<u32x4*>(kr2)[i] = z;
+    reinterpret_cast<u32x4*>(kr3)[i] = z;
+  }
+  for (int j = tid; j < nt; j += kHeatThreads) {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) part[w][j] = REDUCE ? -INFINITY : 0.f;
+    step_list[j] = (j << 8) | min(max(p.valid_count[j], 0), kHalf);
+  }
+  if (wave == 0) {
+    int h1 = 0;
+    for (int j0 = 0; j0 < nt; j0 += 64) {
+      const int j = j0 + lane;
+      const int vc = j < nt ? min(p.valid_count[j], kTile) : 0;
+      const bool two = vc > kHalf;
+      const uint64_t bal = __ballot(two);
+      const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+      if (two) step_list[nt + h1 + rank] = (j << 8) | (1 << 7) | (vc - kHalf);
+      h1 += __builtin_popcountll(bal);
+    }
+    if (lane == 0) step_total = nt + h1;
+  }
+
+  const int vcq = min(max(p.valid_count[qt], 0), kTile);
+  const int row = 32 * qg + li;
+  const bool row_ok = row < vcq;
+  const int64_t qrow = qt * kTile + row;
   bf16x8 qf[8];
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
-    qf[s] = as_bf16x8(*reinterpret_cast<const u32x4*>(p.q + qrow * p.qs + head * p.qh + 16 * s + 8 * hi));
-  const bool row_ok = p.slot_valid[qrow] != 0;
-  const float lse = p.lse[qrow * p.ls + head * p.lh];
-  const float lse2 = row_ok ? lse * kLog2e : INFINITY;   // sum: exp2 domain
-  const float lse_n = row_ok ? lse : INFINITY;           // max: natural domain
+  for (int s = 0; s < 8; ++s) {
+    const u32x4 v = row_ok ? ld16(p.q + qrow * p.qs + head * p.qh + 16 * s + 8 * hi)
+                           : u32x4{0, 0, 0, 0};
+    qf[s] = __builtin_bit_cast(bf16x8, v);
+  }
+#pragma unroll
+  for (int s = 0; s < 8; ++s) asm volatile("" : : "v"(qf[s]));
+  const float lse = row_ok ? p.lse[qrow * p.ls + head * p.lh] : 0.f;
+  // sum: exp2(s * c2 - lse2); an invalid row has lse2 = +inf (adds 0).
   const float c2 = p.scale * kLog2e;
+  const float lse2 = row_ok ? lse * kLog2e : INFINITY;
+  __syncthreads();  // ring, partials and step list ready
+  const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
 
-  u32x4 st[8];
-  int valid;
-  load_k(p, head, j0, tid, st, valid);
-  store_k(kbuf[0], vmask[0], tid, st, valid);
-  __syncthreads();
-  for (int t = 0; t < nt; ++t) {
-    if (t + 1 < nt) load_k(p, head, j0 + t + 1, tid, st, valid);
-    const uint8_t* kb = kbuf[t & 1];
-    const uint64_t vm[2] = {vmask[t & 1][0], vmask[t & 1][1]};
-    float acc = p.reduce ? -INFINITY : 0.f;
+  uint32_t kfo[8];  // K fragment offsets: row 32 kh + li, logical chunk 2s + hi
+  {
+    const uint32_t krow = (32 * kh + li) * 256, x = (hi ^ (li & 15)) << 4;
 #pragma unroll
-    for (int t2 = 0; t2 < 4; ++t2) {
-      f32x16 sacc;
+    for (int s = 0; s < 8; ++s) kfo[s] = krow + (x ^ (s << 5));
+  }
+  const KDma dma = kdma_offsets(p.ks, wave, lane);
+  const uint16_t* kbase = p.k + head * p.kh;
+  auto word = [&](int u) { return __builtin_amdgcn_readfirstlane(step_list[u]); };
+  auto load_step = [&](int u, lds_u8* slot) {
+    const int wd = word(u);
+    const int64_t row0 = (int64_t)(wd >> 8) * kTile + ((wd >> 7) & 1) * kHalf;
+    const int vch = wd & 127;
+    const char* b = reinterpret_cast<const char*>(kbase + row0 * p.ks);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
-      const int krow = 32 * t2 + li;
-      const uint8_t* kr = kb + krow * 256;
+    for (int s = 0; s < 2; ++s) {
+      const int seg = 2 * wave + s;
+      dma16(b, 4 * seg < vch ? dma.k[s] : dma.skip[s], slot + seg * 1024);
+    }
+  };
+  auto compute_step = [&](int u, const lds_u8* slot) {
+    const int wd = word(u);
+    const int j = wd >> 8, vch = wd & 127;
+    if (vch <= 32 * kh) return;  // this wave's 32 keys are all padding
+    u32x4 kf[8];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const int ch = 2 * s + hi;
-        bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(kr + ((ch ^ (krow & 15)) << 4)));
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc, 0, 0, 0);
-      }
-      // Register e holds key 32 t2 + 8 (e / 4) + 4 hi + e % 4.
+    for (int s = 0; s < 8; ++s)
+      kf[s] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(slot + kfo[s]);
+    f32x16 sacc;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = 32 * t2 + 8 * (e >> 2) + 4 * hi + (e & 3);
-        const bool kv = (vm[key >> 6] >> (key & 63)) & 1ull;
-        if (p.reduce) {
-          acc = kv ? fmaxf(acc, sacc[e]) : acc;
-        } else {
-          acc += kv ? __builtin_amdgcn_exp2f(sacc[e] * c2 - lse2) : 0.f;
-        }
-      }
+    for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kf[s]), qf[s],
+                                                     sacc, 0, 0, 0);
+    // Register e holds key 32 kh + 8 (e / 4) + 4 hi + e % 4 of the half.
+    if (vch < 32 * (kh + 1)) {
+      const int lim = vch - 32 * kh - 4 * hi;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (8 * (e >> 2) + (e & 3) >= lim) sacc[e] = -INFINITY;
     }
     float v;
-    if (p.reduce) {
-      // Row max over the block, rounded to bf16 like the reference's bf16
-      // scores (rounding is monotonic, so rounding the max is rounding all).
-      float rm = fmaxf(acc, __shfl_xor(acc, 32, 64));
+    if (REDUCE) {
+      // Row max over the step's keys, rounded to bf16 like the reference's
+      // bf16 scores (rounding is monotonic, so rounding the max is rounding
+      // every score), then max over rows of max * scale - lse.
+      float rm = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) rm = fmaxf(rm, sacc[e]);
       if (rm != -INFINITY) rm = bf16_to_f32(f32_to_bf16(rm));
-      v = rm * p.scale - lse_n;
-      if (rm == -INFINITY || !row_ok) v = -INFINITY;
-#pragma unroll
-      for (int m = 16; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+      v = (rm == -INFINITY || !row_ok) ? -INFINITY : rm * p.scale - lse;
+      v = wave_reduce<true>(v);
     } else {
-      v = acc;
+      float a[4];
 #pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+      for (int g = 0; g < 4; ++g) {
+        a[g] = 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) a[g] += __builtin_amdgcn_exp2f(fmaf(sacc[4 * g + m], c2, -lse2));
+      }
+      v = wave_reduce<false>((a[0] + a[1]) + (a[2] + a[3]));
     }
-    if (lane == 0) part[wave][t] = v;
-    if (t + 1 < nt) store_k(kbuf[(t + 1) & 1], vmask[(t + 1) & 1], tid, st, valid);
-    __syncthreads();
+    if (lane == 0) part[wave][j] = REDUCE ? fmaxf(part[wave][j], v) : part[wave][j] + v;
+  };
+  // The ring: step u in slot u & 3; at the top of step u its own two loads
+  // per wave are waited for (those of u+1, u+2 may stay in flight), then a
+  // bare barrier (as in the attention kernel), then the slot step u-1 used is
+  // refilled with step u+3.
+  auto top = [&](int u) {
+    if (u + 2 < n_steps) VEDA_WAIT_VM(4);
+    else if (u + 1 < n_steps) VEDA_WAIT_VM(2);
+    else VEDA_WAIT_VM(0);
+    __builtin_amdgcn_s_barrier();
+  };
+  if (n_steps > 0) load_step(0, K0);
+  if (n_steps > 1) load_step(1, K1);
+  if (n_steps > 2) load_step(2, K2);
+  for (int u = 0; u < n_steps; u += 4) {
+    top(u);
+    if (u + 3 < n_steps) load_step(u + 3, K3);
+    compute_step(u, K0);
+    if (u + 1 >= n_steps) break;
+    top(u + 1);
+    if (u + 4 < n_steps) load_step(u + 4, K0);
+    compute_step(u + 1, K1);
+    if (u + 2 >= n_steps) break;
+    top(u + 2);
+    if (u + 5 < n_steps) load_step(u + 5, K1);
+    compute_step(u + 2, K2);
+    if (u + 3 >= n_steps) break;
+    top(u + 3);
+    if (u + 6 < n_steps) load_step(u + 6, K2);
+    compute_step(u + 3, K3);
   }
-  if (tid < nt) {
-    float v = part[0][tid];
-    if (p.reduce) {
-      for (int w = 1; w < 4; ++w) v = fmaxf(v, part[w][tid]);
-      v = v == -INFINITY ? 0.f : expf(v);
-    } else {
-      for (int w = 1; w < 4; ++w) v += part[w][tid];
-    }
-    p.heat[(head * p.n_q + r) * p.n_tiles + j0 + tid] = v;
+  __syncthreads();  // all partials written
+  for (int j = tid; j < nt; j += kHeatThreads) {
+    float v = part[0][j];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) v = REDUCE ? fmaxf(v, part[w][j]) : v + part[w][j];
+    if (REDUCE) v = v == -INFINITY ? 0.f : expf(v);
+    heat_row[j] = v;
   }
 }
 
@@ -166,7 +251,7 @@ using namespace veda;
 extern "C" int veda_block_heat(const void* q, int64_t q_stride_s, int64_t q_stride_h,
                                const void* k, int64_t k_stride_s, int64_t k_stride_h,
                                const float* lse, int64_t lse_stride_s, int64_t lse_stride_h,
-                               const int32_t* slot_valid, const int64_t* q_tiles, int64_t n_q,
+                               const int32_t* valid_count, const int64_t* q_tiles, int64_t n_q,
                                int64_t n_tiles, int64_t n_heads, int64_t head_dim, int reduce,
                                float scale, float* heat, void* stream) {
   VEDA_REQUIRE(head_dim == kD, "block_heat: head_dim must be 128, got %lld", (long long)head_dim);
@@ -176,18 +261,20 @@ extern "C" int veda_block_heat(const void* q, int64_t q_stride_s, int64_t q_stri
                    (reinterpret_cast<uintptr_t>(k) & 15) == 0,
                "block_heat: rows must be 16-byte aligned");
   VEDA_REQUIRE(n_q >= 0 && n_tiles >= 0 && n_heads >= 0, "block_heat: negative size");
+  VEDA_REQUIRE(n_tiles <= kMaxTiles, "block_heat: %lld key tiles, at most %d",
+               (long long)n_tiles, kMaxTiles);
   if (n_q == 0 || n_tiles == 0 || n_heads == 0) return VEDA_OK;
   HeatParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.k = static_cast<const uint16_t*>(k);
   p.qs = q_stride_s; p.qh = q_stride_h; p.ks = k_stride_s; p.kh = k_stride_h;
   p.lse = lse; p.ls = lse_stride_s; p.lh = lse_stride_h;
-  p.slot_valid = slot_valid; p.q_tiles = q_tiles;
+  p.valid_count = valid_count; p.q_tiles = q_tiles;
   p.n_q = n_q; p.n_tiles = n_tiles; p.n_heads = n_heads;
-  p.n_groups = (n_tiles + kTilesPerGroup - 1) / kTilesPerGroup;
-  p.reduce = reduce; p.scale = scale; p.heat = heat;
-  const int64_t items = n_heads * n_q * p.n_groups;
+  p.scale = scale; p.heat = heat;
+  const int64_t items = n_heads * n_q;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  heat_kernel<<<(unsigned)items, kHeatThreads, 0, s>>>(p);
+  if (reduce) heat_kernel<1><<<(unsigned)items, kHeatThreads, 0, s>>>(p);
+  else heat_kernel<0><<<(unsigned)items, kHeatThreads, 0, s>>>(p);
   return check_launch("veda_block_heat");
 }

@@ -148,4 +148,4 @@ def teacher_heat(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor,
                  reduce: str = 'max') -> torch.Tensor:
     """[H', R, n_tiles] fp32 block heat ('max' peak / 'sum' mass) of query
     tiles `q_tiles` (heatmap.py:36-110)."""
-    return ops.block_heat(q, k, lse, layout.slot_valid, q_tiles, reduce)
+    return ops.block_heat(q, k, lse, layout.valid_count, q_tiles, reduce)

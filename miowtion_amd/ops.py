@@ -297,9 +297,11 @@ def _(q, k, v, used, return_lse):
 
 
 @torch.library.custom_op('veda::block_heat', mutates_args=())
-def block_heat(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, slot_valid: torch.Tensor,
+def block_heat(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, valid_count: torch.Tensor,
                q_tiles: torch.Tensor, reduce: str) -> torch.Tensor:
-    _require_gpu(q, k, lse, slot_valid, q_tiles)
+    """[H', R, n_tiles] fp32 block heat; the real rows of tile t are its first
+    valid_count[t] slots (the tile layout's prefix rule)."""
+    _require_gpu(q, k, lse, valid_count, q_tiles)
     if reduce not in ('max', 'sum'):
         raise ValueError(f"reduce must be 'max' or 'sum': {reduce!r}")
     _check_rows('q', q)
@@ -310,11 +312,13 @@ def block_heat(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, slot_valid: 
         raise ValueError('lse must be fp32 [N, H\']')
     n_slots, heads, d = q.shape
     n_tiles = n_slots // TILE
+    if valid_count.numel() != n_tiles or valid_count.dtype != torch.int32:
+        raise ValueError(f'valid_count must be int32 [{n_tiles}]')
     qt = q_tiles.to(torch.int64).contiguous()
     heat = torch.empty(heads, qt.numel(), n_tiles, dtype=torch.float32, device=q.device)
     _native.call('veda_block_heat', q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
                  k.stride(0), k.stride(1), lse.data_ptr(), lse.stride(0), lse.stride(1),
-                 slot_valid.data_ptr(), qt.data_ptr(), qt.numel(), n_tiles, heads, d,
+                 valid_count.contiguous().data_ptr(), qt.data_ptr(), qt.numel(), n_tiles, heads, d,
                  1 if reduce == 'max' else 0, 1.0 / math.sqrt(d), heat.data_ptr(), _stream(q))
     return heat
 

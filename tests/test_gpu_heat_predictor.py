@@ -61,6 +61,54 @@ def test_heat_rejects_unknown_reduction():
         kernels.teacher_heat(qt.cuda(), kt.cuda(), lse_t.cuda(), lay, rows.cuda(), 'mean')
 
 
+def test_heat_edge_cases_out_of_range_rows_and_empty_key_tiles():
+    """A q_tiles entry outside the layout gets a zero row; a key tile with no
+    real row (here: one whose keys were masked out by zeroing its valid
+    count) gets zero heat in both reductions, and partial key tiles count
+    only their real keys (the row-mass identity holds)."""
+    lay, olay, qt, kt, lse_t, rows = _heat_case()
+    n = lay.n_tiles
+    rows2 = torch.tensor([0, n, -1, n - 1])
+    for reduce in ('sum', 'max'):
+        got = kernels.teacher_heat(qt.cuda(), kt.cuda(), lse_t.cuda(), lay, rows2.cuda(),
+                                   reduce).cpu()
+        assert torch.equal(got[:, 1], torch.zeros_like(got[:, 1]))
+        assert torch.equal(got[:, 2], torch.zeros_like(got[:, 2]))
+        ok = torch.tensor([0, n - 1])
+        ref = oa.teacher_heat(qt, kt, lse_t, olay, ok, reduce, score_dtype=torch.float32)
+        if reduce == 'sum':
+            torch.testing.assert_close(got[:, [0, 3]], ref, rtol=1e-4, atol=1e-7)
+        else:
+            ref16 = oa.teacher_heat(qt, kt, lse_t, olay, ok, reduce, score_dtype=torch.bfloat16)
+            torch.testing.assert_close(got[:, [0, 3]], ref16, rtol=2e-3, atol=1e-7)
+
+
+def test_heat_at_config5_size_sampled_rows():
+    """BASELINE config 5 geometry (2,048 global rows + 102x30x52, (1,8,16)
+    tiles, 1,648 key tiles): heat('sum') of sampled query tiles of two heads
+    against the fp32-score oracle on the same LSE, to 1e-4 relative, and the
+    row-mass identity sum_j heat = valid rows."""
+    spans, used, seq_len, shape = helpers.CONFIGS['C5']
+    lay = helpers.product_layout(spans, used, seq_len, shape, device='cuda')
+    olay = helpers.oracle_layout(spans, used, seq_len, shape)
+    g = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn(seq_len, 2, 128, generator=g).to(torch.bfloat16) for _ in range(3))
+    q[used:] = 0
+    k[used:] = 0
+    v[used:] = 0
+    _, lse = kernels.dense_attention(q.cuda(), k.cuda(), v.cuda(), used, return_lse=True)
+    heads = torch.arange(2)
+    qt, kt = (kernels.gather_tiles(t.cuda(), lay, None) for t in (q, k))
+    lse_t = kernels.gather_lse(lse, lay, heads.cuda())
+    rows = torch.tensor([0, 15, 16, 700, lay.n_tiles - 1])
+    got = kernels.teacher_heat(qt, kt, lse_t, lay, rows.cuda(), 'sum').cpu()
+    ref = oa.teacher_heat(qt.cpu(), kt.cpu(), lse_t.cpu(), olay, rows, 'sum',
+                          score_dtype=torch.float32)
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-7)
+    want = olay.valid_count[rows].float()
+    torch.testing.assert_close(got.sum(-1), want.expand(2, -1), rtol=1e-3, atol=1e-3)
+
+
 def _predictor_case(fp8, second=0, count=False, seed=0):
     spec = helpers.small_layout()
     lay = helpers.product_layout(*spec, device='cuda')
