@@ -166,6 +166,47 @@ def test_predictor_logits_match_oracle(fp8, second, count):
     assert torch.equal(sel.index.cpu(), idx) and torch.equal(sel.keep.cpu(), keep)
 
 
+@pytest.mark.parametrize('contiguous', [False, True])
+def test_config4_predictor_and_selection_at_config2_geometry(contiguous):
+    """BASELINE config 4 at config-2 size: 57,720 tokens, (1,8,16) tiles (592
+    tiles, or the contiguous tiler's 451), fp8 e4m3 projections with per-head
+    scales (~N(0, 0.02) before quantisation), 90% top-k with the forced
+    diagonal. Two heads. Pooled features and logits match the oracle (max /
+    min bit-exact, mean 1e-5, logits 1e-4 of scale); the selection from the
+    kernel's logits is bit-exact to the oracle's selection on the same
+    logits; against the oracle's own logits at most a small fraction of the
+    kept blocks flips (near-ties in fp32 summation order)."""
+    spans, used, seq_len, shape = helpers.CONFIGS['C2']
+    lay = helpers.product_layout(spans, used, seq_len, shape, device='cuda', contiguous=contiguous)
+    olay = helpers.oracle_layout(spans, used, seq_len, shape, contiguous=contiguous)
+    assert lay.n_tiles == (451 if contiguous else 592)
+    q, k = helpers.qkv(seq_len, 2, 128, seed=4, n=2)
+    heads = torch.arange(2)
+    pred = pp.LayerPredictor.random(2, 128, std=0.02, generator=torch.Generator().manual_seed(5),
+                                    device='cuda', fp8=True)
+    _, fq = kernels.gather_and_pool(q.cuda(), lay, heads.cuda())
+    _, fk = kernels.gather_and_pool(k.cuda(), lay, heads.cuda())
+    ofq = op.pool_tiles(ot.gather_tiles(q, olay, heads), olay)
+    ofk = op.pool_tiles(ot.gather_tiles(k, olay, heads), olay)
+    d = 128
+    for got, want in ((fq.cpu(), ofq), (fk.cpu(), ofk)):
+        torch.testing.assert_close(got[..., :d], want[..., :d], rtol=1e-5, atol=1e-6)
+        assert torch.equal(got[..., d:], want[..., d:])
+    got = pred(fq, fk, heads.cuda()).cpu()
+    want = op.logits(ofq, ofk, _oracle_weight(pred.proj_q), _oracle_weight(pred.proj_k), heads)
+    assert (got - want).abs().max() <= 1e-4 * want.abs().max() + 1e-6
+    nv = lay.n_video_tiles
+    sel = pm.select_video_blocks(got[:, :nv].cuda(), lay, pm.column_blocks(lay, pm.Budget(ratio=0.1)))
+    idx, keep = om.select_video_blocks(got[:, :nv], olay, om.column_blocks(olay, om.Budget(ratio=0.1)))
+    assert torch.equal(sel.index.cpu(), idx) and torch.equal(sel.keep.cpu(), keep)
+    mask_got = om.dense_block_mask(idx, keep, olay)
+    idx2, keep2 = om.select_video_blocks(want[:, :nv], olay, om.column_blocks(olay, om.Budget(ratio=0.1)))
+    mask_ref = om.dense_block_mask(idx2, keep2, olay)
+    flips = int((mask_got != mask_ref).sum()) / max(int(mask_ref.sum()), 1)
+    print(f'config 4 ({lay.n_tiles} tiles): kept-block flip rate vs oracle logits {flips:.2e}')
+    assert flips < 1e-2
+
+
 def test_e4m3_decode_matches_torch_for_every_code():
     """Every finite e4m3 code decodes as torch's float8_e4m3fn does (the two
     NaN codes are left out: a NaN weight poisons its whole output column)."""
