@@ -245,6 +245,15 @@ def suite(reps: int = 5) -> dict:
     rows5 = torch.arange(nv5, device='cuda')
     ms = _median_ms(lambda: kernels.teacher_heat(qt5, kt5, lse_t, lay5, rows5, 'sum'), 3)
     res['heat_sum_c5'] = _mfma(ms, 2.0 * 128 * 128 * D * nv5 * n5 * HEADS)
+    # the fused teacher pass in tile order: LSE + heat from one QK^T pass
+    # (what OracleStudent runs instead of dense_fwd_lse + heat), and the same
+    # pass with the dense output as well
+    ms_f = _median_ms(lambda: kernels.dense_heat(qt5, kt5, lay5, rows5, 'sum'), 3)
+    res['dense_heat_sum_c5'] = _mfma(ms_f, 2.0 * 128 * 128 * D * nv5 * n5 * HEADS)
+    res['dense_heat_sum_c5']['two_pass_ms'] = round(res['dense_fwd_lse_c5']['ms'] +
+                                                    res['heat_sum_c5']['ms'], 4)
+    ms_o = _median_ms(lambda: kernels.dense_heat(qt5, kt5, lay5, rows5, 'sum', v=vt5), 3)
+    res['dense_heat_out_sum_c5'] = _mfma(ms_o, 4.0 * 128 * 128 * D * nv5 * n5 * HEADS)
     heat = kernels.teacher_heat(qt5, kt5, lse_t, lay5, rows5, 'sum')
     blocks5 = pm.column_blocks(lay5, pm.Budget(ratio=0.05))
     sel5 = pm.select_video_blocks(heat[:, :, :nv5], lay5, blocks5, rows5)

@@ -205,6 +205,48 @@ int veda_block_heat(const void* q, int64_t q_stride_s, int64_t q_stride_h,
                     float* heat, void* stream);
 
 /*
+ * Teacher dense pass in tile order with the block-heat statistics: the
+ * fused form of the dense LSE pass (miowtion/h3/attention.py:80-102, as
+ * OracleStudent uses it, miowtion/veda/attention.py:549-553) and the heat
+ * (miowtion/veda/heatmap.py:36-110), the plan of
+ * docs/features/veda_kernel.md:285-289.
+ *
+ * Item r (of n_items) is query tile q_tiles[r] (NULL: tile r) of q, which
+ * holds q_tiles_held tiles; it attends to every valid key (the first
+ * valid_count[j] slots of key tile j) of n_k_tiles key tiles. Writes
+ *   lse[h * lse_stride_h + (128 r + s) * lse_stride_s]  natural-log LSE,
+ *   part[(h * n_k_tiles + j) * (128 n_items) + 128 r + s]  (fp32, log2
+ *     units) the row's log-sum-exp ('sum', reduce 0) or max ('max', reduce
+ *     1) of scale * q.k over the valid keys of tile j (-inf if none),
+ * and, when out and v are both non-NULL, the attention output in tile order
+ * out[128 r + s, h, :]. part is caller workspace of n_heads * n_k_tiles *
+ * 128 n_items floats. Then veda_heat_combine gives the heat.
+ */
+int veda_dense_heat_fwd(const void* q, int64_t q_stride_s, int64_t q_stride_h,
+                        int64_t q_tiles_held, const void* k, int64_t k_stride_s,
+                        int64_t k_stride_h, const void* v, int64_t v_stride_s,
+                        int64_t v_stride_h, int64_t n_heads, int64_t head_dim,
+                        const int64_t* q_tiles, int64_t n_items, int64_t n_k_tiles,
+                        const int32_t* valid_count, float scale, int reduce,
+                        void* out, int64_t o_stride_s, int64_t o_stride_h,
+                        float* lse, int64_t lse_stride_h, int64_t lse_stride_s,
+                        float* part, void* stream);
+
+/*
+ * Block heat from veda_dense_heat_fwd's statistics
+ * (miowtion/veda/heatmap.py:36-110 semantics; miowtion/kernels/
+ * block_heat_triton.py:141-173 computes the same from a separate LSE):
+ *   'sum' (0): heat[h, r, j] = sum over the valid rows s of 2^(part - lse log2 e)
+ *   'max' (1): heat[h, r, j] = 2^(max over the valid rows of (part - lse log2 e))
+ * heat: fp32 [n_heads, n_items, n_tiles] contiguous; rows with lse = -inf
+ * and slots past valid_count[q_tiles[r]] count as absent.
+ */
+int veda_heat_combine(const float* part, const float* lse, int64_t lse_stride_h,
+                      int64_t lse_stride_s, const int32_t* valid_count,
+                      const int64_t* q_tiles, int64_t n_items, int64_t n_tiles,
+                      int64_t n_heads, int reduce, float* heat, void* stream);
+
+/*
  * Predictor tile embedding, miowtion/veda/predictor.py:251-255:
  *   out[h', t, :] = feats[h', t, :] @ W[heads[h']] (+ feats[h', t, :n_out]
  *   when residual), fp32 accumulation.

@@ -6,8 +6,10 @@ bf16 with padding rows zero.
   SparseStudent  (miowtion/veda/attention.py:692-794): gather + pool q/k,
                  gather v, predictor logits, top-k, block mask, block-sparse
                  attention, scatter -- all HIP kernels.
-  OracleStudent  (miowtion/veda/attention.py:478-588): dense attention with
-                 LSE, teacher heat, top-k on heat, block-sparse attention.
+  OracleStudent  (miowtion/veda/attention.py:478-588): the teacher's LSE and
+                 block heat (one fused QK pass in tile order by default;
+                 dense attention + heat kernel with fused=False), top-k on
+                 heat, block-sparse attention.
   DenseAttention (miowtion/h3/model.py:48-58): the dense kernel.
 
 Heads are processed per plan head group (<= 2 shapes per layer) and in
@@ -188,15 +190,25 @@ class SparseStudent:
 
 
 class OracleStudent:
-    """Block sparsity masked by the true block statistic (attention.py:478-588)."""
+    """Block sparsity masked by the true block statistic (attention.py:478-588).
 
-    def __init__(self, clip: ClipTiling, plan: veda_plan.TilePlan, target: str = 'mass'):
+    The reference runs dense attention for its LSE only (its output is
+    discarded, attention.py:549-553) and then recomputes QK^T for the heat.
+    With `fused` (the default) one pass over the tile-ordered q / k gives
+    both: the LSE and a per-(key tile, row) statistic that an HBM-bound
+    kernel turns into the heat (the fusion docs/features/veda_kernel.md:
+    285-289 plans). `fused=False` keeps the reference's two passes.
+    """
+
+    def __init__(self, clip: ClipTiling, plan: veda_plan.TilePlan, target: str = 'mass',
+                 fused: bool = True):
         if target not in ORACLE_TARGETS:
             raise ValueError(f'target must be one of {ORACLE_TARGETS}: {target!r}')
         _require_kernels(clip.device, 'OracleStudent')
         self.clip = clip
         self.plan = plan
         self.target = target
+        self.fused = fused
         self.calls = {'sparse': 0, 'dense': 0}
         self.last: dict = {}
 
@@ -206,8 +218,10 @@ class OracleStudent:
             self.calls['dense'] += 1
             return kernels.dense_attention(q, k, v, used)[0]
         self.calls['sparse'] += 1
-        with torch.no_grad():
-            _, lse = kernels.dense_attention(q, k, v, used, return_lse=True)
+        lse = None
+        if not self.fused:
+            with torch.no_grad():
+                _, lse = kernels.dense_attention(q, k, v, used, return_lse=True)
         seq_len = q.shape[0]
         out = q.new_zeros(seq_len + 1, *q.shape[1:])
         self.last = {'lse': lse}
@@ -227,8 +241,13 @@ class OracleStudent:
         rows = torch.arange(tile_layout.n_video_tiles, device=q.device)
         with torch.no_grad():
             reduce = 'max' if self.target == 'max' else 'sum'
-            heat = kernels.teacher_heat(q_tiles, k_tiles, kernels.gather_lse(lse, tile_layout, heads),
-                                        tile_layout, rows, reduce)
+            lse_tiles = None
+            if self.fused:
+                heat, lse_tiles, _ = kernels.dense_heat(q_tiles, k_tiles, tile_layout, rows, reduce)
+            else:
+                heat = kernels.teacher_heat(q_tiles, k_tiles,
+                                            kernels.gather_lse(lse, tile_layout, heads),
+                                            tile_layout, rows, reduce)
             if self.target == 'mean':
                 counts = tile_layout.valid_count.clamp(min=1).to(heat.dtype)
                 heat = heat / counts[None, None, :]
@@ -240,4 +259,5 @@ class OracleStudent:
                                                      tile_layout)
         kernels.scatter_tiles_(out, o_tiles, tile_layout, heads)
         self.last.setdefault('parts', []).append(
-            dict(shape=tile_layout, heads=heads, heat=heat, selection=selection))
+            dict(shape=tile_layout, heads=heads, heat=heat, selection=selection,
+                 lse_tiles=lse_tiles))

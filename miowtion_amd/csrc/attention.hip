@@ -62,7 +62,22 @@ struct FwdParams {
   int64_t os, oh;
   float* lse;
   int64_t lse_sh, lse_ss;
+  // All-tiles walk only: query tile of item r (NULL: tile r), and the
+  // per-(key tile, query row) block statistic [H'][n_k][items * 128] in
+  // log2 units (block log-sum-exp for heat 'sum', block max for 'max').
+  const int64_t* q_tiles;
+  int64_t q_tiles_held;  // tiles q holds; an item whose q_tiles entry is outside reads zeros
+  float* part;
+  int64_t part_sh, part_st;
 };
+
+// Key walks: the block lists (sparse forward), every row of a packed
+// sequence (dense forward), or every key tile of a tile layout in order,
+// its padding rows masked (the teacher's dense pass in tile order).
+enum Walk { kLists = 0, kDense = 1, kAllTiles = 2 };
+// Block statistic collected for the teacher heat: none, log-sum-exp, max.
+enum Heat { kNoHeat = 0, kHeatSum = 1, kHeatMax = 2 };
+constexpr int32_t kTileEnd = 1 << 30;  // step-list flag: last step of its key tile
 
 
 // Per-wave state: Q^T fragments of the wave's 32 rows (lane (li, hi) holds
@@ -72,6 +87,8 @@ struct WaveState {
   bf16x8 qf[8];
   f32x16 o[4];
   float m_run, l_run;
+  float mu;     // exponent offset of the last step computed
+  float blk;    // heat: the current key tile's partial (sum relative to mu, or max)
 };
 
 // ---------------------------------------------------------------------------
@@ -127,8 +144,8 @@ __device__ __forceinline__ HDma hdma_offsets(int64_t ks, int64_t vs, int wave, i
 // Issues the loads of the step at key row row0 (64 rows, the first vch >= 1
 // of them valid) into `slot`. CLAMP (the dense path's last tile, whose rows past the
 // valid count may lie past the end of k / v): every lane reads a row below
-// vch instead.
-template <bool CLAMP>
+// vch instead. Without PV only K is loaded.
+template <bool CLAMP, bool PV>
 __device__ __forceinline__ void issue_step(const uint16_t* kbase, const uint16_t* vbase,
                                            const FwdParams& p, const HDma& d, int64_t row0,
                                            int vch, int wave, int lane, lds_u8* slot) {
@@ -149,7 +166,7 @@ __device__ __forceinline__ void issue_step(const uint16_t* kbase, const uint16_t
       vo = live ? d.v[u] : d.v_skip[u];
     }
     dma16(kb, ko, slot + seg * 1024);
-    dma16(vb, vo, slot + kHalfBytes + seg * 1024);
+    if (PV) dma16(vb, vo, slot + kHalfBytes + seg * 1024);
   }
 }
 
@@ -178,6 +195,7 @@ __device__ __forceinline__ HFrag hfrag_offsets(int kh, int lane) {
 
 // One step for this wave's 32 rows and 32 keys from `slot`; keys at or past
 // vch (of the half) are masked.
+template <int HEAT, bool PV>
 __device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float c, int vch,
                                       int kh, int hi, WaveState& w) {
   u32x4 kf[8];
@@ -205,18 +223,26 @@ __device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float 
   float mloc = -INFINITY;
 #pragma unroll
   for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
-  mloc = half_swap_max(mloc) * c;
+  const float mraw = half_swap_max(mloc);  // unscaled row max over the wave's 32 keys
+  mloc = mraw * c;
   const float m_new = mloc > w.m_run + kRescaleSlack ? mloc : w.m_run;
   const float mu = m_new == -INFINITY ? 0.f : m_new;
   const float alpha = __builtin_amdgcn_exp2f(w.m_run - mu);
   w.m_run = m_new;
+  w.mu = mu;
+  // heat 'max': the wave's unscaled row max over its keys of the tile
+  if (HEAT == kHeatMax) w.blk = fmaxf(w.blk, mraw);
   float ps[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) ps[e] = __builtin_amdgcn_exp2f(fmaf(s[e], c, -mu));
   float l4[4];
 #pragma unroll
   for (int g = 0; g < 4; ++g) l4[g] = (ps[4 * g] + ps[4 * g + 1]) + (ps[4 * g + 2] + ps[4 * g + 3]);
-  w.l_run = fmaf(w.l_run, alpha, (l4[0] + l4[1]) + (l4[2] + l4[3]));
+  const float lsum = (l4[0] + l4[1]) + (l4[2] + l4[3]);
+  w.l_run = fmaf(w.l_run, alpha, lsum);
+  // heat 'sum': this lane's 16 keys, relative to mu like l
+  if (HEAT == kHeatSum) w.blk = fmaf(w.blk, alpha, lsum);
+  if (!PV) return;
   u32x4 pk[2];
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)
@@ -243,14 +269,17 @@ __device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float 
 }
 
 
-template <bool DENSE>
+template <int WALK, int HEAT, bool PV>
 __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
+  constexpr bool DENSE = WALK == kDense;
+  constexpr bool TILES = WALK == kAllTiles;
   __shared__ __attribute__((aligned(1024))) uint8_t slot0[kSlotBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t slot1[kSlotBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t slot2[kSlotBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t slot3[kSlotBytes];
   __shared__ int32_t step_list[2 * kMaxBlocks];
   __shared__ int32_t step_total;
+  __shared__ float lbuf[2][4][32];  // heat: kh = 1 hands its key-tile partials to kh = 0
   lds_u8* sl0 = (lds_u8*)slot0;
   lds_u8* sl1 = (lds_u8*)slot1;
   lds_u8* sl2 = (lds_u8*)slot2;
@@ -262,7 +291,11 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   const int64_t item = blockIdx.x;
   const int64_t head = item / p.n_q_tiles;
   const int64_t r = item % p.n_q_tiles;
-  const int64_t qrow = r * kTile + 32 * qg + li;
+  const int64_t qrow = r * kTile + 32 * qg + li;  // row of out / lse / part
+  // row of q (the all-tiles walk reads query tile q_tiles[r])
+  const int64_t qtile = TILES && p.q_tiles != nullptr ? p.q_tiles[r] : r;
+  const bool qtile_ok = !TILES || (qtile >= 0 && qtile < p.q_tiles_held);
+  const int64_t qsrc = TILES ? (qtile_ok ? qtile : 0) * kTile + 32 * qg + li : qrow;
 
   // Zero the ring (stale rows are multiplied by p = 0 only; see above).
   for (int i = tid; i < kSlotBytes / 16; i += kThreads) {
@@ -285,6 +318,30 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   if (DENSE) {
     const int64_t nsteps = (p.used + kHalf - 1) / kHalf;
     n_steps = (int)nsteps;
+  } else if (TILES) {
+    // Every key tile in order, its steps consecutive: the first half, then
+    // the second half when more than 64 keys are valid; the tile's last step
+    // carries kTileEnd. An empty tile is one step with no valid key.
+    if (wave == 0) {
+      const int nk = (int)p.n_k_tiles;
+      int base = 0;
+      for (int j0 = 0; j0 < nk; j0 += 64) {
+        const int j = j0 + lane;
+        const int vc = j < nk ? min(max(p.valid_count[j], 0), kTile) : 0;
+        const bool two = j < nk && vc > kHalf;
+        const uint64_t bal = __ballot(two);
+        const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+        if (j < nk) {
+          const int at = base + lane + rank;
+          const int32_t row0 = j * kTile;
+          step_list[at] = (row0 << 7) | min(vc, kHalf) | (two ? 0 : kTileEnd);
+          if (two) step_list[at + 1] = ((row0 + kHalf) << 7) | (vc - kHalf) | kTileEnd;
+        }
+        base += min(64, nk - j0) + __builtin_popcountll(bal);
+      }
+      if (lane == 0) step_total = base;
+    }
   } else {
     const int64_t li_ = head * p.n_q_tiles + r;
     const int ld = (int)p.list_ld;
@@ -327,8 +384,8 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   WaveState w;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
-    const bool q_ok = DENSE ? (qrow < p.used) : true;
-    u32x4 v = q_ok ? ld16(p.q + qrow * p.qs + head * p.qh + 16 * s + 8 * hi) : u32x4{0, 0, 0, 0};
+    const bool q_ok = DENSE ? (qrow < p.used) : qtile_ok;
+    u32x4 v = q_ok ? ld16(p.q + qsrc * p.qs + head * p.qh + 16 * s + 8 * hi) : u32x4{0, 0, 0, 0};
     w.qf[s] = as_bf16x8(v);
   }
 #pragma unroll
@@ -339,12 +396,15 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
     for (int e = 0; e < 16; ++e) w.o[dt][e] = 0.f;
   w.m_run = -INFINITY;
   w.l_run = 0.f;
+  w.mu = 0.f;
+  w.blk = HEAT == kHeatMax ? -INFINITY : 0.f;
   __syncthreads();  // step list, step count and zeroed ring ready
   if (!DENSE) n_steps = __builtin_amdgcn_readfirstlane(step_total);
 
   // (first key row, valid keys) of step u
   auto step_row = [&](int u) -> int64_t {
-    return DENSE ? (int64_t)u * kHalf : (int64_t)(__builtin_amdgcn_readfirstlane(step_list[u]) >> 7);
+    return DENSE ? (int64_t)u * kHalf
+                 : (int64_t)((__builtin_amdgcn_readfirstlane(step_list[u]) >> 7) & 0x7FFFFF);
   };
   auto step_vch = [&](int u) -> int {
     if (DENSE) {
@@ -364,9 +424,9 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
     // a step with no valid key (an empty or out-of-range tile) loads the
     // tile's first rows, which exist; its keys are all masked
     if (DENSE && vch < kHalf)
-      issue_step<true>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
+      issue_step<true, PV>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
     else
-      issue_step<false>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
+      issue_step<false, PV>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
   };
   // Prologue: steps 0, 1, 2 into slots 0, 1, 2.
   if (n_steps > 0) load_step(0, sl0);
@@ -381,16 +441,61 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   // for its own loads, and every fragment read of the previous step has been
   // consumed by an MFMA before its wave reaches the barrier.
   auto wait_step = [&](int u) {
-    if (u + 2 < n_steps) VEDA_WAIT_VM(8);
-    else if (u + 1 < n_steps) VEDA_WAIT_VM(4);
+    // loads per wave per step: 4 (K and V), 2 without PV
+    if (u + 2 < n_steps) VEDA_WAIT_VM(PV ? 8 : 4);
+    else if (u + 1 < n_steps) VEDA_WAIT_VM(PV ? 4 : 2);
     else VEDA_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
   };
   // A wave whose 32 keys of the step are all padding skips the step: all
   // its scores would be -inf, which leaves m, l and O unchanged.
+  // Heat partials. At the end of a key tile each wave turns its partial
+  // into a log2 statistic of its rows over its keys of the tile: the
+  // log-sum-exp ('sum': log2 of the sum, relative to mu, plus mu) or the
+  // max ('max'). kh = 1 leaves it in LDS; kh = 0 combines it with its own
+  // after the next barrier and writes one value per (key tile, row).
+  int pend_j = -1;
+  float pend_l = 0.f;
+  auto flush_tile = [&](int j) {
+    float l;
+    if (HEAT == kHeatSum) {
+      const float tot = half_swap_sum(w.blk);
+      l = tot > 0.f ? __log2f(tot) + w.mu : -INFINITY;
+      w.blk = 0.f;
+    } else {
+      // the reference rounds the unscaled max to the input dtype (bf16) and
+      // scales after it (block_heat_triton.py:131-133, heatmap.py:88-95)
+      l = bf16_to_f32(f32_to_bf16(w.blk)) * c;
+      w.blk = -INFINITY;
+    }
+    if (kh == 1) {
+      if (hi == 0) lbuf[j & 1][qg][li] = l;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // visible at the next barrier
+    } else {
+      pend_l = l;
+      pend_j = j;
+    }
+  };
+  auto write_pending = [&]() {
+    const float l1 = lbuf[pend_j & 1][qg][li];
+    float l;
+    if (HEAT == kHeatSum) {
+      const float a = fmaxf(pend_l, l1), b = fminf(pend_l, l1);
+      l = a == -INFINITY ? -INFINITY : a + __log2f(1.f + __builtin_amdgcn_exp2f(b - a));
+    } else {
+      l = fmaxf(pend_l, l1);
+    }
+    if (hi == 0) p.part[head * p.part_sh + (int64_t)pend_j * p.part_st + qrow] = l;
+    pend_j = -1;
+  };
   auto compute_step = [&](int u, const lds_u8* slot) {
     const int vch = step_vch(u);
-    if (vch > 32 * kh) hstep(slot, frag, c, vch, kh, hi, w);
+    if (HEAT != kNoHeat && kh == 0 && pend_j >= 0) write_pending();
+    if (vch > 32 * kh) hstep<HEAT, PV>(slot, frag, c, vch, kh, hi, w);
+    if (HEAT != kNoHeat) {
+      const int32_t word = __builtin_amdgcn_readfirstlane(step_list[u]);
+      if (word & kTileEnd) flush_tile((word >> 7 & 0x7FFFFF) / kTile);
+    }
   };
   for (int u = 0; u < n_steps; u += 4) {
     wait_step(u);
@@ -410,6 +515,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
     compute_step(u + 3, sl3);
   }
   __syncthreads();  // every wave is done reading the ring
+  if (HEAT != kNoHeat && kh == 0 && pend_j >= 0) write_pending();
 
   // Merge the two key halves: kh = 1 hands (m, l, O) to kh = 0 through LDS.
   w.l_run = half_swap_sum(w.l_run);
@@ -417,10 +523,12 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   float* red = reinterpret_cast<float*>(qg < 2 ? slot0 : slot1) + (qg & 1) * 64 * 64;
   float* ml = reinterpret_cast<float*>(slot2);  // [qg][m | l][32]
   if (kh == 1) {
+    if (PV) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) red[(dt * 16 + e) * 64 + lane] = w.o[dt][e];
+        for (int e = 0; e < 16; ++e) red[(dt * 16 + e) * 64 + lane] = w.o[dt][e];
+    }
     if (hi == 0) {
       ml[qg * 64 + li] = w.m_run;
       ml[qg * 64 + 32 + li] = w.l_run;
@@ -438,7 +546,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   if (qrow >= p.q_rows) return;  // dense mode: rows past seq_len do not exist
   uint16_t* orow = p.out + qrow * p.os + head * p.oh;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < (PV ? 4 : 0); ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float v4[4];
@@ -512,7 +620,7 @@ extern "C" int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t 
   p.os = o_stride_s; p.oh = o_stride_h;
   p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hfwd_kernel<false><<<(unsigned)items, kThreads, 0, s>>>(p);
+  hfwd_kernel<kLists, kNoHeat, true><<<(unsigned)items, kThreads, 0, s>>>(p);
   return check_launch("veda_block_sparse_fwd");
 }
 
@@ -550,6 +658,69 @@ extern "C" int veda_dense_fwd(const void* q, int64_t q_stride_s, int64_t q_strid
   p.os = o_stride_s; p.oh = o_stride_h;
   p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hfwd_kernel<true><<<(unsigned)items, kThreads, 0, s>>>(p);
+  hfwd_kernel<kDense, kNoHeat, true><<<(unsigned)items, kThreads, 0, s>>>(p);
   return check_launch("veda_dense_fwd");
+}
+
+extern "C" int veda_dense_heat_fwd(const void* q, int64_t q_stride_s, int64_t q_stride_h,
+                                   int64_t q_tiles_held, const void* k, int64_t k_stride_s,
+                                   int64_t k_stride_h, const void* v, int64_t v_stride_s,
+                                   int64_t v_stride_h, int64_t n_heads, int64_t head_dim,
+                                   const int64_t* q_tiles, int64_t n_items, int64_t n_k_tiles,
+                                   const int32_t* valid_count, float scale, int reduce,
+                                   void* out, int64_t o_stride_s, int64_t o_stride_h, float* lse,
+                                   int64_t lse_stride_h, int64_t lse_stride_s, float* part,
+                                   void* stream) {
+  VEDA_REQUIRE(head_dim == kD, "dense_heat_fwd: head_dim must be 128, got %lld",
+               (long long)head_dim);
+  VEDA_REQUIRE(reduce == 0 || reduce == 1, "dense_heat_fwd: reduce must be 0 (sum) or 1 (max)");
+  VEDA_REQUIRE(n_heads >= 0 && n_items >= 0 && q_tiles_held >= 0,
+               "dense_heat_fwd: negative size");
+  VEDA_REQUIRE(q_tiles != nullptr || n_items <= q_tiles_held,
+               "dense_heat_fwd: %lld items but q holds %lld tiles", (long long)n_items,
+               (long long)q_tiles_held);
+  VEDA_REQUIRE(lse != nullptr && part != nullptr, "dense_heat_fwd: lse and part are required");
+  VEDA_REQUIRE((out == nullptr) == (v == nullptr),
+               "dense_heat_fwd: out and v go together (out needs P.V)");
+  VEDA_REQUIRE(aligned16(q) && aligned16(k) && (v == nullptr || aligned16(v)) &&
+                   (out == nullptr || aligned16(out)) && q_stride_s % 8 == 0 &&
+                   q_stride_h % 8 == 0 && k_stride_s % 8 == 0 && k_stride_h % 8 == 0 &&
+                   (v == nullptr || (v_stride_s % 8 == 0 && v_stride_h % 8 == 0)) &&
+                   (out == nullptr || (o_stride_s % 4 == 0 && o_stride_h % 4 == 0)),
+               "dense_heat_fwd: rows must be 16-byte aligned");
+  const int64_t items = n_heads * n_items;
+  if (items == 0) return VEDA_OK;
+  VEDA_REQUIRE(n_k_tiles >= 1 && n_k_tiles <= kMaxBlocks,
+               "dense_heat_fwd: n_k_tiles %lld outside [1, %d]", (long long)n_k_tiles, kMaxBlocks);
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = v != nullptr ? static_cast<const uint16_t*>(v) : p.k;
+  p.qs = q_stride_s; p.qh = q_stride_h;
+  p.ks = k_stride_s; p.kh = k_stride_h;
+  p.vs = v != nullptr ? v_stride_s : k_stride_s;
+  p.vh = v != nullptr ? v_stride_h : k_stride_h;
+  p.n_heads = n_heads; p.n_q_tiles = n_items; p.n_k_tiles = n_k_tiles;
+  p.valid_count = valid_count;
+  p.used = 0;
+  p.q_rows = n_items * kTile;
+  p.scale_log2 = (float)((double)scale * 1.4426950408889634);
+  p.out = static_cast<uint16_t*>(out);
+  p.os = o_stride_s; p.oh = o_stride_h;
+  p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
+  p.q_tiles = q_tiles;
+  p.q_tiles_held = q_tiles_held;
+  p.part = part;
+  p.part_st = n_items * kTile;
+  p.part_sh = n_k_tiles * p.part_st;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const unsigned g = (unsigned)items;
+  if (out != nullptr) {
+    if (reduce) hfwd_kernel<kAllTiles, kHeatMax, true><<<g, kThreads, 0, s>>>(p);
+    else hfwd_kernel<kAllTiles, kHeatSum, true><<<g, kThreads, 0, s>>>(p);
+  } else {
+    if (reduce) hfwd_kernel<kAllTiles, kHeatMax, false><<<g, kThreads, 0, s>>>(p);
+    else hfwd_kernel<kAllTiles, kHeatSum, false><<<g, kThreads, 0, s>>>(p);
+  }
+  return check_launch("veda_dense_heat_fwd");
 }

@@ -243,6 +243,54 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
   }
 }
 
+// Heat from the block statistics of the teacher's dense pass in tile order
+// (veda_dense_heat_fwd): part[h][j][row] is the log2 log-sum-exp ('sum') or
+// log2 max ('max') of query row `row` over the valid keys of key tile j,
+// lse[h][row] the row's natural-log LSE over all keys. Then
+//   'sum': heat[h, r, j] = sum over valid rows of 2^(part - lse log2 e)
+//   'max': heat[h, r, j] = 2^(max over valid rows of (part - lse log2 e))
+// (0 when nothing is valid), the block's softmax mass / peak probability.
+// Workgroup = (head, query item), 4 waves; wave w takes key tiles w, w + 4,
+// ..., each a 512-byte coalesced read of the item's 128 rows.
+template <bool REDUCE>
+__global__ void __launch_bounds__(256) heat_combine_kernel(
+    const float* __restrict__ part, const float* __restrict__ lse, int64_t ls_h, int64_t ls_s,
+    const int32_t* __restrict__ valid_count, const int64_t* __restrict__ q_tiles,
+    int64_t n_items, int64_t n_tiles, float* __restrict__ heat) {
+  const int64_t item = blockIdx.x;
+  const int64_t h = item / n_items, r = item % n_items;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t qt = q_tiles != nullptr ? q_tiles[r] : r;
+  const int vc = (qt >= 0 && qt < n_tiles) ? valid_count[qt] : 0;
+  float l2[2];
+  bool ok[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int slot = lane + 64 * x;
+    const float l = lse[h * ls_h + (r * kTile + slot) * ls_s];
+    ok[x] = slot < vc && l != -INFINITY;
+    l2[x] = l * kLog2e;
+  }
+  const int64_t rows = n_items * kTile;
+  const float* base = part + h * n_tiles * rows + r * kTile;
+  float* out = heat + (h * n_items + r) * n_tiles;
+  for (int64_t j = wave; j < n_tiles; j += 4) {
+    const float* pr = base + j * rows;
+    const float x0 = pr[lane], x1 = pr[lane + 64];
+    float v;
+    if (REDUCE) {
+      v = fmaxf(ok[0] ? x0 - l2[0] : -INFINITY, ok[1] ? x1 - l2[1] : -INFINITY);
+      v = wave_reduce<true>(v);
+      v = v == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(v);
+    } else {
+      v = (ok[0] ? __builtin_amdgcn_exp2f(x0 - l2[0]) : 0.f) +
+          (ok[1] ? __builtin_amdgcn_exp2f(x1 - l2[1]) : 0.f);
+      v = wave_reduce<false>(v);
+    }
+    if (lane == 0) out[j] = v;
+  }
+}
+
 }  // namespace
 }  // namespace veda
 
@@ -277,4 +325,22 @@ extern "C" int veda_block_heat(const void* q, int64_t q_stride_s, int64_t q_stri
   if (reduce) heat_kernel<1><<<(unsigned)items, kHeatThreads, 0, s>>>(p);
   else heat_kernel<0><<<(unsigned)items, kHeatThreads, 0, s>>>(p);
   return check_launch("veda_block_heat");
+}
+
+extern "C" int veda_heat_combine(const float* part, const float* lse, int64_t lse_stride_h,
+                                 int64_t lse_stride_s, const int32_t* valid_count,
+                                 const int64_t* q_tiles, int64_t n_items, int64_t n_tiles,
+                                 int64_t n_heads, int reduce, float* heat, void* stream) {
+  VEDA_REQUIRE(reduce == 0 || reduce == 1, "heat_combine: reduce must be 0 (sum) or 1 (max)");
+  VEDA_REQUIRE(n_items >= 0 && n_tiles >= 0 && n_heads >= 0, "heat_combine: negative size");
+  if (n_items == 0 || n_tiles == 0 || n_heads == 0) return VEDA_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const unsigned g = (unsigned)(n_heads * n_items);
+  if (reduce)
+    heat_combine_kernel<true><<<g, 256, 0, s>>>(part, lse, lse_stride_h, lse_stride_s, valid_count,
+                                                q_tiles, n_items, n_tiles, heat);
+  else
+    heat_combine_kernel<false><<<g, 256, 0, s>>>(part, lse, lse_stride_h, lse_stride_s,
+                                                 valid_count, q_tiles, n_items, n_tiles, heat);
+  return check_launch("veda_heat_combine");
 }

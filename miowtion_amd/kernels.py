@@ -149,3 +149,22 @@ def teacher_heat(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor,
     """[H', R, n_tiles] fp32 block heat ('max' peak / 'sum' mass) of query
     tiles `q_tiles` (heatmap.py:36-110)."""
     return ops.block_heat(q, k, lse, layout.valid_count, q_tiles, reduce)
+
+
+def dense_heat(q: torch.Tensor, k: torch.Tensor, layout: tiling.TileLayout,
+               q_tiles: torch.Tensor, reduce: str = 'max', v: torch.Tensor | None = None):
+    """The teacher's dense pass in tile order, fused with the block heat.
+
+    One pass over every valid key of the layout gives, for the query tiles
+    `q_tiles`, the row LSE and a per-(key tile, row) log2 statistic; a second,
+    HBM-bound kernel turns those into the heat of heatmap.py:36-110 (the
+    same values as teacher_heat with the dense LSE). With `v` the pass also
+    returns the dense output in tile order (the form
+    docs/features/veda_kernel.md:285-289 plans for the teacher).
+
+    Returns:
+        (heat [H', R, n] fp32, lse [H', R * 128] fp32, out [R * 128, H', D]
+        bf16 or None).
+    """
+    res = ops.dense_heat(q, k, v, layout.valid_count, q_tiles, reduce)
+    return res[0], res[1], (res[2] if v is not None else None)

@@ -328,6 +328,83 @@ def _(q, k, lse, slot_valid, q_tiles, reduce):
     return q.new_empty(q.shape[1], q_tiles.numel(), q.shape[0] // TILE, dtype=torch.float32)
 
 
+# Teacher dense pass in tile order with the heat statistics
+# (miowtion/veda/attention.py:549-588, the fused form of
+# docs/features/veda_kernel.md:285-289).
+
+# Workspace bound of the per-(key tile, query row) statistics: heads are
+# processed in chunks whose workspace stays below this.
+HEAT_WORKSPACE_BYTES = 4 * 2 ** 30
+
+
+@torch.library.custom_op('veda::dense_heat', mutates_args=())
+def dense_heat(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None,
+               valid_count: torch.Tensor, q_tiles: torch.Tensor, reduce: str,
+               workspace_bytes: int = HEAT_WORKSPACE_BYTES) -> list[torch.Tensor]:
+    """Dense attention of the query tiles `q_tiles` over every valid key of a
+    tile layout, in one pass that also yields the block heat.
+
+    q, k (and v): tile-ordered [N, H', 128] bf16; q_tiles: [R] tile ids.
+    Returns [heat [H', R, n] fp32, lse [H', R*128] fp32 (natural log)] and,
+    when v is given, out [R*128, H', 128] bf16 as a third entry.
+    """
+    _require_gpu(q, k, v, valid_count, q_tiles)
+    if reduce not in ('max', 'sum'):
+        raise ValueError(f"reduce must be 'max' or 'sum': {reduce!r}")
+    _check_rows('q', q)
+    _check_rows('k', k)
+    if v is not None:
+        _check_rows('v', v)
+        if v.shape != k.shape:
+            raise ValueError('v must match k')
+    if q.shape[-1] != 128 or k.shape != q.shape:
+        raise ValueError("dense_heat needs equal [N, H', 128] q and k")
+    n_slots, heads, d = q.shape
+    if n_slots % TILE:
+        raise ValueError(f'{n_slots} rows is not a whole number of {TILE}-row tiles')
+    n_tiles = n_slots // TILE
+    if valid_count.numel() != n_tiles or valid_count.dtype != torch.int32:
+        raise ValueError(f'valid_count must be int32 [{n_tiles}]')
+    qt = q_tiles.to(torch.int64).contiguous()
+    n_items = qt.numel()
+    if n_items and (int(qt.min()) < 0 or int(qt.max()) >= n_tiles):
+        raise ValueError(f'q_tiles outside [0, {n_tiles})')
+    heat = torch.empty(heads, n_items, n_tiles, dtype=torch.float32, device=q.device)
+    lse = torch.empty(heads, n_items * TILE, dtype=torch.float32, device=q.device)
+    out = None if v is None else q.new_empty(n_items * TILE, heads, d)
+    per_head = n_tiles * n_items * TILE * 4
+    chunk = max(1, min(heads, workspace_bytes // max(per_head, 1)))
+    part = torch.empty(chunk * per_head // 4, dtype=torch.float32, device=q.device)
+    vc = valid_count.contiguous()
+    for h0 in range(0, heads, chunk):
+        h1 = min(heads, h0 + chunk)
+        qh, kh = q[:, h0:h1], k[:, h0:h1]
+        vh = None if v is None else v[:, h0:h1]
+        oh = None if out is None else out[:, h0:h1]
+        _native.call('veda_dense_heat_fwd', qh.data_ptr(), qh.stride(0), qh.stride(1), n_tiles,
+                     kh.data_ptr(), kh.stride(0), kh.stride(1), _p(vh),
+                     0 if vh is None else vh.stride(0), 0 if vh is None else vh.stride(1),
+                     h1 - h0, d, qt.data_ptr(), n_items, n_tiles, vc.data_ptr(),
+                     1.0 / math.sqrt(d), 1 if reduce == 'max' else 0, _p(oh),
+                     0 if oh is None else oh.stride(0), 0 if oh is None else oh.stride(1),
+                     lse[h0:h1].data_ptr(), lse.stride(0), lse.stride(1), part.data_ptr(),
+                     _stream(q))
+        _native.call('veda_heat_combine', part.data_ptr(), lse[h0:h1].data_ptr(), lse.stride(0),
+                     lse.stride(1), vc.data_ptr(), qt.data_ptr(), n_items, n_tiles, h1 - h0,
+                     1 if reduce == 'max' else 0, heat[h0:h1].data_ptr(), _stream(q))
+    return [heat, lse] if out is None else [heat, lse, out]
+
+
+@dense_heat.register_fake
+def _(q, k, v, valid_count, q_tiles, reduce, workspace_bytes=HEAT_WORKSPACE_BYTES):
+    n = q.shape[0] // TILE
+    res = [q.new_empty(q.shape[1], q_tiles.numel(), n, dtype=torch.float32),
+           q.new_empty(q.shape[1], q_tiles.numel() * TILE, dtype=torch.float32)]
+    if v is not None:
+        res.append(q.new_empty(q_tiles.numel() * TILE, q.shape[1], q.shape[2]))
+    return res
+
+
 # --------------------------------------------------------------------------
 # predictor (miowtion/veda/predictor.py:251-338)
 

@@ -104,20 +104,28 @@ def test_sparse_student_dynamic_shapes_and_round_trip():
     _close(out[:used], want[:used])
 
 
-def test_oracle_student_matches_oracle_chain():
+@pytest.mark.parametrize('fused', [True, False])
+def test_oracle_student_matches_oracle_chain(fused):
     spec = helpers.small_layout(grid=(6, 12, 20), shape='2x8x8', text=100, extra=16)
     spans, used, seq_len, shape = spec
     clip = _clip(spans, used, seq_len, 0.3)
     plan = pplan.TilePlan.uniform('o', spans[-1][1], pt.TileShape.parse(shape), 1, 4)
-    student = pa.OracleStudent(clip, plan, target='mass')
+    student = pa.OracleStudent(clip, plan, target='mass', fused=fused)
     q, k, v = helpers.qkv(seq_len, 4, 128, seed=2)
     out = student(q.cuda(), k.cuda(), v.cuda(), 0).cpu()
     olay = helpers.oracle_layout(*spec)
     heads = torch.arange(4)
     _, lse = oa.dense_attention(q, k, v, used, return_lse=True)
-    _close(student.last['lse'], lse)
-    qt, kt = ot.gather_tiles(q, olay, heads), ot.gather_tiles(k, olay, heads)
     rows = torch.arange(olay.n_video_tiles)
+    if fused:
+        # the tile-ordered LSE of the fused pass, on the real rows
+        got = student.last['parts'][0]['lse_tiles'].cpu()
+        want = ot.gather_lse(lse, olay, heads)[:rows.numel() * 128].t()
+        real = olay.slot_valid[:rows.numel() * 128].bool()
+        torch.testing.assert_close(got[:, real], want[:, real], rtol=0, atol=2e-4)
+    else:
+        _close(student.last['lse'], lse)
+    qt, kt = ot.gather_tiles(q, olay, heads), ot.gather_tiles(k, olay, heads)
     # select on the kernel's heat: the selection is then bit-exact
     heat = student.last['parts'][0]['heat'].cpu()
     ref_heat = oa.teacher_heat(qt, kt, ot.gather_lse(lse, olay, heads), olay, rows, 'sum')
