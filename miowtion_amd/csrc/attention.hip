@@ -273,11 +273,18 @@ template <int WALK, int HEAT, bool PV>
 __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   constexpr bool DENSE = WALK == kDense;
   constexpr bool TILES = WALK == kAllTiles;
-  __shared__ __attribute__((aligned(1024))) uint8_t slot0[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t slot1[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t slot2[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t slot3[kSlotBytes];
-  __shared__ int32_t step_list[2 * kMaxBlocks];
+  // Without PV a slot holds K only, and the all-tiles walk keeps its steps
+  // as 16-bit (tile, half) entries plus a byte per tile of valid counts:
+  // the statistics-only pass then needs 75 KB of LDS, so two workgroups
+  // share a CU and hide each other's latencies.
+  constexpr int kSlot = PV ? kSlotBytes : kHalfBytes;
+  __shared__ __attribute__((aligned(1024))) uint8_t slot0[kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t slot1[kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t slot2[kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t slot3[kSlot];
+  __shared__ int32_t step_list[TILES ? 1 : 2 * kMaxBlocks];
+  __shared__ uint16_t tile_steps[TILES ? 2 * kMaxBlocks : 1];  // (key tile << 1) | half
+  __shared__ uint8_t tile_valid[TILES ? kMaxBlocks : 1];
   __shared__ int32_t step_total;
   __shared__ float lbuf[2][4][32];  // heat: kh = 1 hands its key-tile partials to kh = 0
   lds_u8* sl0 = (lds_u8*)slot0;
@@ -298,7 +305,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   const int64_t qsrc = TILES ? (qtile_ok ? qtile : 0) * kTile + 32 * qg + li : qrow;
 
   // Zero the ring (stale rows are multiplied by p = 0 only; see above).
-  for (int i = tid; i < kSlotBytes / 16; i += kThreads) {
+  for (int i = tid; i < kSlot / 16; i += kThreads) {
     reinterpret_cast<u32x4*>(slot0)[i] = u32x4{0, 0, 0, 0};
     reinterpret_cast<u32x4*>(slot1)[i] = u32x4{0, 0, 0, 0};
     reinterpret_cast<u32x4*>(slot2)[i] = u32x4{0, 0, 0, 0};
@@ -334,9 +341,9 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
         if (j < nk) {
           const int at = base + lane + rank;
-          const int32_t row0 = j * kTile;
-          step_list[at] = (row0 << 7) | min(vc, kHalf) | (two ? 0 : kTileEnd);
-          if (two) step_list[at + 1] = ((row0 + kHalf) << 7) | (vc - kHalf) | kTileEnd;
+          tile_valid[j] = (uint8_t)vc;
+          tile_steps[at] = (uint16_t)(j << 1);
+          if (two) tile_steps[at + 1] = (uint16_t)((j << 1) | 1);
         }
         base += min(64, nk - j0) + __builtin_popcountll(bal);
       }
@@ -401,17 +408,28 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   __syncthreads();  // step list, step count and zeroed ring ready
   if (!DENSE) n_steps = __builtin_amdgcn_readfirstlane(step_total);
 
+  // Step word of step u: (first key row << 7) | valid keys | kTileEnd.
+  auto step_word = [&](int u) -> int32_t {
+    if (TILES) {
+      const int e = __builtin_amdgcn_readfirstlane(tile_steps[u]);
+      const int j = e >> 1, half = e & 1;
+      const int vc = __builtin_amdgcn_readfirstlane(tile_valid[j]);
+      const int vch = half ? vc - kHalf : min(vc, kHalf);
+      return ((j * kTile + half * kHalf) << 7) | vch | ((half || vc <= kHalf) ? kTileEnd : 0);
+    }
+    return __builtin_amdgcn_readfirstlane(step_list[u]);
+  };
   // (first key row, valid keys) of step u
   auto step_row = [&](int u) -> int64_t {
     return DENSE ? (int64_t)u * kHalf
-                 : (int64_t)((__builtin_amdgcn_readfirstlane(step_list[u]) >> 7) & 0x7FFFFF);
+                 : (int64_t)((step_word(u) >> 7) & 0x7FFFFF);
   };
   auto step_vch = [&](int u) -> int {
     if (DENSE) {
       const int64_t rem = p.used - (int64_t)u * kHalf;
       return rem < kHalf ? (int)rem : kHalf;
     }
-    return __builtin_amdgcn_readfirstlane(step_list[u]) & 127;
+    return step_word(u) & 127;
   };
   const uint16_t* kbase = p.k + head * p.kh;
   const uint16_t* vbase = p.v + head * p.vh;
@@ -493,7 +511,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
     if (HEAT != kNoHeat && kh == 0 && pend_j >= 0) write_pending();
     if (vch > 32 * kh) hstep<HEAT, PV>(slot, frag, c, vch, kh, hi, w);
     if (HEAT != kNoHeat) {
-      const int32_t word = __builtin_amdgcn_readfirstlane(step_list[u]);
+      const int32_t word = step_word(u);
       if (word & kTileEnd) flush_tile((word >> 7 & 0x7FFFFF) / kTile);
     }
   };
