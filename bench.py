@@ -195,6 +195,15 @@ def suite(reps: int = 5) -> dict:
     ms = _median_ms(lambda: kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'],
                                                                  c['lists'], lay), reps)
     res['sparse_fwd_c2'] = _mfma(ms, 4.0 * 128 * 128 * D * kept)
+    # zero-order compensation of the dropped tiles (summaries + the virtual-key
+    # pass; the reference's Triton form costs 1.14x its sparse kernel)
+    o_kept, lse_kept = kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'], c['lists'],
+                                                            lay, return_lse=True)
+    ms_c = _median_ms(lambda: kernels.zero_order_compensation(o_kept, lse_kept, c['qt'], c['kt'],
+                                                              c['vt'], c['mask'], lay), reps)
+    res['compensation_c2'] = _mfma(ms_c, 4.0 * c['qt'].shape[0] * n * D * HEADS)
+    res['compensation_c2']['vs_sparse_fwd'] = round((ms + ms_c) / ms, 3)
+    del o_kept, lse_kept
     ms = _median_ms(lambda: kernels.dense_attention(q, c['k'], v, used, return_lse=True), 3)
     res['dense_fwd_lse_c2'] = _mfma(ms, 4.0 * used * used * HEADS * D)
     del c, outbuf, fq, fk

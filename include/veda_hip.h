@@ -247,6 +247,41 @@ int veda_heat_combine(const float* part, const float* lse, int64_t lse_stride_h,
                       int64_t n_heads, int reduce, float* heat, void* stream);
 
 /*
+ * Tile summaries of the zero-order compensation
+ * (miowtion/kernels/compensation_triton.py:80-99, :150-170): for key tile t
+ * and head h, kc[t, h, :] = mean of k over the tile's real rows (sum /
+ * max(valid_count[t], 1)) and vc[t, h, :] = their sum of v, both bf16.
+ * k, v: bf16 [n_tiles * 128, n_heads, 128]; kc, vc: bf16 [n_tiles, n_heads,
+ * 128] with strides (c_stride_s, c_stride_h, 1).
+ */
+int veda_tile_summaries(const void* k, int64_t k_stride_s, int64_t k_stride_h,
+                        const void* v, int64_t v_stride_s, int64_t v_stride_h,
+                        const int32_t* valid_count, int64_t n_tiles,
+                        int64_t n_heads, int64_t head_dim, void* kc, void* vc,
+                        int64_t c_stride_s, int64_t c_stride_h, void* stream);
+
+/*
+ * Zero-order compensation (miowtion/veda/attention.py:591-689; the Triton
+ * form miowtion/kernels/compensation_triton.py:102-147, :173-225): for row
+ * r of query tile i and head h,
+ *   p_j = exp(q[r] . kc[j] * scale - lse_kept[h, r])   (lse_kept -> 0 if not finite)
+ *   out[r] = (o_kept[r] + sum_j p_j vc[j]) / (1 + sum_j p_j valid_count[j])
+ * over the key tiles j with keep[h, i, j] == 0 and valid_count[j] > 0.
+ * keep: bytes [n_heads, n_q_tiles, n_k_tiles]; o_kept, q, out: bf16
+ * [n_q_tiles * 128, n_heads, 128]; kc, vc from veda_tile_summaries.
+ */
+int veda_zero_order_compensation(const void* o_kept, int64_t ok_stride_s,
+                                 int64_t ok_stride_h, const float* lse_kept,
+                                 int64_t lse_stride_h, int64_t lse_stride_s,
+                                 const void* q, int64_t q_stride_s, int64_t q_stride_h,
+                                 const void* kc, const void* vc, int64_t c_stride_s,
+                                 int64_t c_stride_h, const uint8_t* keep,
+                                 const int32_t* valid_count, int64_t n_heads,
+                                 int64_t head_dim, int64_t n_q_tiles, int64_t n_k_tiles,
+                                 float scale, void* out, int64_t o_stride_s,
+                                 int64_t o_stride_h, void* stream);
+
+/*
  * Predictor tile embedding, miowtion/veda/predictor.py:251-255:
  *   out[h', t, :] = feats[h', t, :] @ W[heads[h']] (+ feats[h', t, :n_out]
  *   when residual), fp32 accumulation.

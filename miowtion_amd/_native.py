@@ -38,6 +38,9 @@ SIGNATURES: dict[str, list] = {
     'veda_dense_heat_fwd': [_P, _I, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _P, _I, _I,
                             _P, _F, _C, _P, _I, _I, _P, _I, _I, _P, _P],
     'veda_heat_combine': [_P, _P, _I, _I, _P, _P, _I, _I, _I, _C, _P, _P],
+    'veda_tile_summaries': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _P, _P, _I, _I, _P],
+    'veda_zero_order_compensation': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _P, _I, _I, _P, _P,
+                                     _I, _I, _I, _I, _F, _P, _I, _I, _P],
     'veda_predictor_embed': [_P, _I, _I, _I, _P, _C, _P, _I, _P, _I, _C, _P, _P],
     'veda_predictor_logits': [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _C, _P, _P],
 }

@@ -48,6 +48,25 @@ class VedaConfig:
     contiguous_tiles: bool = False
     dense_layers: frozenset = frozenset()
     collect_bytes: int = DEFAULT_COLLECT_BYTES
+    # Zero-order compensation of the dropped tiles (attention.py:70-93).
+    # zero_order_compensation (torch form) and triton_compensation (the
+    # kernel form with bf16 tile summaries) are the same arithmetic and both
+    # run the `veda::zero_order_compensation` HIP kernel here;
+    # fused_compensation is the Sol INT8 kernel, which this build does not
+    # have (refused, not replaced).
+    zero_order_compensation: bool = False
+    triton_compensation: bool = False
+    fused_compensation: bool = False
+
+    def __post_init__(self):
+        chosen = [n for n in ('zero_order_compensation', 'fused_compensation',
+                              'triton_compensation') if getattr(self, n)]
+        if len(chosen) > 1:
+            raise ValueError(f'at most one compensation arm may be set, got {chosen}')
+        if self.fused_compensation:
+            raise NotImplementedError('fused_compensation (the Sol INT8 kernel) is not part of '
+                                      'this build; zero_order_compensation computes the same '
+                                      'term around the block-sparse kernel')
 
 
 @dataclasses.dataclass(frozen=True)
@@ -181,8 +200,16 @@ class SparseStudent:
                 logits[:, :tile_layout.n_video_tiles], tile_layout, self.clip.blocks(tile_layout))
             block_mask = veda_mask.dense_block_mask(selection, tile_layout)
             lists = kernels.index_lists(block_mask, tile_layout)
-            o_tiles = kernels.block_sparse_attention_lists(q_tiles, k_tiles, v_tiles, lists,
-                                                           tile_layout)
+            cfg = self.clip.config
+            if cfg.zero_order_compensation or cfg.triton_compensation:
+                o_kept, lse_kept = kernels.block_sparse_attention_lists(
+                    q_tiles, k_tiles, v_tiles, lists, tile_layout, return_lse=True)
+                o_tiles = kernels.zero_order_compensation(
+                    o_kept, lse_kept, q_tiles, k_tiles, v_tiles,
+                    block_mask & tile_layout.kv_ok[None, None, :], tile_layout)
+            else:
+                o_tiles = kernels.block_sparse_attention_lists(q_tiles, k_tiles, v_tiles, lists,
+                                                               tile_layout)
         kernels.scatter_tiles_(out, o_tiles, tile_layout, heads)
         self.last.setdefault('parts', []).append(
             dict(shape=tile_layout, heads=heads, selection=selection, lists=lists,

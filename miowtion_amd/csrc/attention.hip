@@ -66,7 +66,14 @@ struct FwdParams {
   // per-(key tile, query row) block statistic [H'][n_k][items * 128] in
   // log2 units (block log-sum-exp for heat 'sum', block max for 'max').
   const int64_t* q_tiles;
-  int64_t q_tiles_held;  // tiles q holds; an item whose q_tiles entry is outside reads zeros
+  int64_t q_tiles_held;
+  // Virtual-key walk (zero-order compensation) only: the kept-block mask
+  // [H'][items][n_k] (bytes), the kept output o_kept and its LSE lse_kept.
+  const uint8_t* keep;
+  const uint16_t* o_kept;
+  int64_t oks, okh;
+  const float* lse_kept;
+  int64_t lk_h, lk_s;  // tiles q holds; an item whose q_tiles entry is outside reads zeros
   float* part;
   int64_t part_sh, part_st;
 };
@@ -74,7 +81,7 @@ struct FwdParams {
 // Key walks: the block lists (sparse forward), every row of a packed
 // sequence (dense forward), or every key tile of a tile layout in order,
 // its padding rows masked (the teacher's dense pass in tile order).
-enum Walk { kLists = 0, kDense = 1, kAllTiles = 2 };
+enum Walk { kLists = 0, kDense = 1, kAllTiles = 2, kVirtual = 3 };
 // Block statistic collected for the teacher heat: none, log-sum-exp, max.
 enum Heat { kNoHeat = 0, kHeatSum = 1, kHeatMax = 2 };
 constexpr int32_t kTileEnd = 1 << 30;  // step-list flag: last step of its key tile
@@ -102,11 +109,12 @@ struct WaveState {
 //
 // A step loads and computes only what the key tile holds: rows at or past
 // the tile's valid count are padding (masked by definition), so their 1 KB
-// segments are not fetched (the load is redirected to rows already being
-// fetched, which keeps every wave's load count fixed for the vmcnt waits),
-// and the upper half of a tile with at most 64 valid keys is no step at all.
-// Stale LDS rows only ever meet masked keys (p = 0); the ring is zeroed once
-// so no uninitialised bits are ever multiplied.
+// segments are not fetched from HBM (the load is redirected to rows already
+// being fetched, which keeps every wave's load count fixed for the vmcnt
+// waits, and writes copies of real rows into those LDS rows, so every row a
+// step reads was written by that step), and the upper half of a tile with
+// at most 64 valid keys is no step at all. Rows past the valid count only
+// ever meet masked keys (p = 0).
 //
 // In each step wave (qg, kh) takes keys 32 kh .. 32 kh + 31 of the half:
 // S^T = K Q^T (8 MFMAs), one online-softmax step over its 32 keys, and
@@ -269,10 +277,63 @@ __device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float 
 }
 
 
+// Zero-order compensation step: this wave's 32 virtual keys of the step
+// (tile summaries: key = mean K of a key tile, value = sum V) against its
+// 32 query rows, with the fixed reference ref2 = lse_kept log2 e of the
+// row instead of an online max. wt[j] is the real row count of key tile j
+// if the mask dropped it, else 0: p = exp2(s c - ref2) where wt > 0, the
+// denominator gains p wt, and O^T += V^T P^T as in the attention step.
+__device__ __forceinline__ void vstep(const lds_u8* slot, const HFrag& f, float c,
+                                      const float* wt, int key0, int hi, float ref2,
+                                      WaveState& w) {
+  u32x4 kf[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    kf[k] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(slot + f.k[k]);
+  f32x16 s;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) s[e] = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[k]), w.qf[k], s, 0, 0, 0);
+  // register e holds key key0 + 8 (e / 4) + 4 hi + e % 4
+  float ps[16], den = 0.f;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const f32x4 ww = *reinterpret_cast<const f32x4*>(wt + key0 + 8 * g + 4 * hi);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const float x = ww[m] > 0.f ? __builtin_amdgcn_exp2f(fmaf(s[4 * g + m], c, -ref2)) : 0.f;
+      ps[4 * g + m] = x;
+      den = fmaf(x, ww[m], den);
+    }
+  }
+  w.l_run += den;
+  u32x4 pk[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) pk[kk][m] = pack_bf16x2(ps[8 * kk + 2 * m], ps[8 * kk + 2 * m + 1]);
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const lds_u8* vs = slot + kk * 16 * 256;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + f.v[dt]));
+      const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + 8 * 256 + f.v[dt]));
+      const bf16x8 a =
+          __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
+      w.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pk[kk]), w.o[dt], 0, 0, 0);
+    }
+  }
+}
+
+
 template <int WALK, int HEAT, bool PV>
 __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   constexpr bool DENSE = WALK == kDense;
   constexpr bool TILES = WALK == kAllTiles;
+  constexpr bool VIRT = WALK == kVirtual;
   // Without PV a slot holds K only, and the all-tiles walk keeps its steps
   // as 16-bit (tile, half) entries plus a byte per tile of valid counts:
   // the statistics-only pass then needs 75 KB of LDS, so two workgroups
@@ -285,6 +346,8 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   __shared__ int32_t step_list[TILES ? 1 : 2 * kMaxBlocks];
   __shared__ uint16_t tile_steps[TILES ? 2 * kMaxBlocks : 1];  // (key tile << 1) | half
   __shared__ uint8_t tile_valid[TILES ? kMaxBlocks : 1];
+  // virtual-key walk: per key tile, its real row count if dropped, else 0
+  __shared__ __attribute__((aligned(16))) float vwt[VIRT ? kMaxBlocks + kHalf : 1];
   __shared__ int32_t step_total;
   __shared__ float lbuf[2][4][32];  // heat: kh = 1 hands its key-tile partials to kh = 0
   lds_u8* sl0 = (lds_u8*)slot0;
@@ -304,13 +367,9 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   const bool qtile_ok = !TILES || (qtile >= 0 && qtile < p.q_tiles_held);
   const int64_t qsrc = TILES ? (qtile_ok ? qtile : 0) * kTile + 32 * qg + li : qrow;
 
-  // Zero the ring (stale rows are multiplied by p = 0 only; see above).
-  for (int i = tid; i < kSlot / 16; i += kThreads) {
-    reinterpret_cast<u32x4*>(slot0)[i] = u32x4{0, 0, 0, 0};
-    reinterpret_cast<u32x4*>(slot1)[i] = u32x4{0, 0, 0, 0};
-    reinterpret_cast<u32x4*>(slot2)[i] = u32x4{0, 0, 0, 0};
-    reinterpret_cast<u32x4*>(slot3)[i] = u32x4{0, 0, 0, 0};
-  }
+  // The ring needs no clearing: every step's loads write all 64 rows of
+  // its slot (segments past the valid count re-read real rows), so an MFMA
+  // only ever reads rows its own step wrote.
 
   // Step list: one word per step, (first key row << 7) | valid keys of the
   // step (0..64). Blocks in walk order (full list first): a full key tile
@@ -325,6 +384,17 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   if (DENSE) {
     const int64_t nsteps = (p.used + kHalf - 1) / kHalf;
     n_steps = (int)nsteps;
+  } else if (VIRT) {
+    // Virtual keys 0 .. n_k - 1 in steps of 64; the table is padded with
+    // zero weights to whole steps.
+    const int nk = (int)p.n_k_tiles;
+    n_steps = (nk + kHalf - 1) / kHalf;
+    const uint8_t* keep_row = p.keep + (head * p.n_q_tiles + r) * p.n_k_tiles;
+    for (int j = tid; j < n_steps * kHalf; j += kThreads) {
+      float wj = 0.f;
+      if (j < nk && keep_row[j] == 0) wj = (float)min(max(p.valid_count[j], 0), kTile);
+      vwt[j] = wj;
+    }
   } else if (TILES) {
     // Every key tile in order, its steps consecutive: the first half, then
     // the second half when more than 64 keys are valid; the tile's last step
@@ -406,7 +476,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   w.mu = 0.f;
   w.blk = HEAT == kHeatMax ? -INFINITY : 0.f;
   __syncthreads();  // step list, step count and zeroed ring ready
-  if (!DENSE) n_steps = __builtin_amdgcn_readfirstlane(step_total);
+  if (!DENSE && !VIRT) n_steps = __builtin_amdgcn_readfirstlane(step_total);
 
   // Step word of step u: (first key row << 7) | valid keys | kTileEnd.
   auto step_word = [&](int u) -> int32_t {
@@ -421,12 +491,12 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   };
   // (first key row, valid keys) of step u
   auto step_row = [&](int u) -> int64_t {
-    return DENSE ? (int64_t)u * kHalf
+    return (DENSE || VIRT) ? (int64_t)u * kHalf
                  : (int64_t)((step_word(u) >> 7) & 0x7FFFFF);
   };
   auto step_vch = [&](int u) -> int {
-    if (DENSE) {
-      const int64_t rem = p.used - (int64_t)u * kHalf;
+    if (DENSE || VIRT) {
+      const int64_t rem = (VIRT ? p.n_k_tiles : p.used) - (int64_t)u * kHalf;
       return rem < kHalf ? (int)rem : kHalf;
     }
     return step_word(u) & 127;
@@ -434,6 +504,12 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   const uint16_t* kbase = p.k + head * p.kh;
   const uint16_t* vbase = p.v + head * p.vh;
   const float c = p.scale_log2;
+  // compensation: the row's fixed reference (0 for a row that kept nothing)
+  float ref2 = 0.f;
+  if (VIRT) {
+    const float lk = p.lse_kept[head * p.lk_h + qrow * p.lk_s];
+    ref2 = (lk > -INFINITY && lk < INFINITY) ? lk * 1.4426950408889634f : 0.f;
+  }
   const HDma dma = hdma_offsets(p.ks, p.vs, wave, lane);
   const HFrag frag = hfrag_offsets(kh, lane);
 
@@ -441,7 +517,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
     const int vch = step_vch(u);
     // a step with no valid key (an empty or out-of-range tile) loads the
     // tile's first rows, which exist; its keys are all masked
-    if (DENSE && vch < kHalf)
+    if ((DENSE || VIRT) && vch < kHalf)
       issue_step<true, PV>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
     else
       issue_step<false, PV>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
@@ -509,7 +585,12 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   auto compute_step = [&](int u, const lds_u8* slot) {
     const int vch = step_vch(u);
     if (HEAT != kNoHeat && kh == 0 && pend_j >= 0) write_pending();
-    if (vch > 32 * kh) hstep<HEAT, PV>(slot, frag, c, vch, kh, hi, w);
+    if (VIRT) {
+      // keys past n_k carry weight 0 (the table is padded), so no mask
+      if (vch > 32 * kh) vstep(slot, frag, c, vwt, u * kHalf + 32 * kh, hi, ref2, w);
+    } else if (vch > 32 * kh) {
+      hstep<HEAT, PV>(slot, frag, c, vch, kh, hi, w);
+    }
     if (HEAT != kNoHeat) {
       const int32_t word = step_word(u);
       if (word & kTileEnd) flush_tile((word >> 7 & 0x7FFFFF) / kTile);
@@ -557,24 +638,38 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   const float m1 = ml[qg * 64 + li], l1 = ml[qg * 64 + 32 + li];
   const float m = fmaxf(w.m_run, m1);
   const float mu = m == -INFINITY ? 0.f : m;
-  const float a0 = __builtin_amdgcn_exp2f(w.m_run - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
+  // compensation: both halves share the fixed reference, so they add; the
+  // kept output is num / den over the kept keys with den = 1 at that
+  // reference, hence out = (o_kept + num) / (1 + den)
+  const float a0 = VIRT ? 1.f : __builtin_amdgcn_exp2f(w.m_run - mu);
+  const float a1 = VIRT ? 1.f : __builtin_amdgcn_exp2f(m1 - mu);
   const float l = w.l_run * a0 + l1 * a1;
   const bool row_real = DENSE ? (qrow < p.used) : true;
-  const float inv = (l > 0.f && row_real) ? 1.f / l : 0.f;
+  const float inv = VIRT ? 1.f / (1.f + l) : (l > 0.f && row_real) ? 1.f / l : 0.f;
   if (qrow >= p.q_rows) return;  // dense mode: rows past seq_len do not exist
   uint16_t* orow = p.out + qrow * p.os + head * p.oh;
+  const uint16_t* krow = VIRT ? p.o_kept + qrow * p.oks + head * p.okh : nullptr;
 #pragma unroll
   for (int dt = 0; dt < (PV ? 4 : 0); ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float v4[4];
+      const int d = 32 * dt + 8 * g + 4 * hi;
+      float kept4[4] = {0.f, 0.f, 0.f, 0.f};
+      if (VIRT) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 kv = *reinterpret_cast<const u32x2*>(krow + d);
+        kept4[0] = bf16_to_f32(kv[0] & 0xffffu);
+        kept4[1] = bf16_to_f32(kv[0] >> 16);
+        kept4[2] = bf16_to_f32(kv[1] & 0xffffu);
+        kept4[3] = bf16_to_f32(kv[1] >> 16);
+      }
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int e = 4 * g + rr;
         const float o1 = red[(dt * 16 + e) * 64 + lane];
-        v4[rr] = (w.o[dt][e] * a0 + o1 * a1) * inv;
+        v4[rr] = (kept4[rr] + w.o[dt][e] * a0 + o1 * a1) * inv;
       }
-      const int d = 32 * dt + 8 * g + 4 * hi;
       uint32_t w0 = pack_bf16x2(v4[0], v4[1]), w1 = pack_bf16x2(v4[2], v4[3]);
       typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
       *reinterpret_cast<u32x2*>(orow + d) = u32x2{w0, w1};
@@ -741,4 +836,48 @@ extern "C" int veda_dense_heat_fwd(const void* q, int64_t q_stride_s, int64_t q_
     else hfwd_kernel<kAllTiles, kHeatSum, false><<<g, kThreads, 0, s>>>(p);
   }
   return check_launch("veda_dense_heat_fwd");
+}
+
+extern "C" int veda_zero_order_compensation(
+    const void* o_kept, int64_t ok_stride_s, int64_t ok_stride_h, const float* lse_kept,
+    int64_t lse_stride_h, int64_t lse_stride_s, const void* q, int64_t q_stride_s,
+    int64_t q_stride_h, const void* kc, const void* vc, int64_t c_stride_s, int64_t c_stride_h,
+    const uint8_t* keep, const int32_t* valid_count, int64_t n_heads, int64_t head_dim,
+    int64_t n_q_tiles, int64_t n_k_tiles, float scale, void* out, int64_t o_stride_s,
+    int64_t o_stride_h, void* stream) {
+  VEDA_REQUIRE(head_dim == kD, "zero_order_compensation: head_dim must be 128, got %lld",
+               (long long)head_dim);
+  VEDA_REQUIRE(n_heads >= 0 && n_q_tiles >= 0, "zero_order_compensation: negative size");
+  VEDA_REQUIRE(aligned16(q) && aligned16(kc) && aligned16(vc) && aligned16(out) &&
+                   (reinterpret_cast<uintptr_t>(o_kept) & 7u) == 0 && q_stride_s % 8 == 0 &&
+                   q_stride_h % 8 == 0 && c_stride_s % 8 == 0 && c_stride_h % 8 == 0 &&
+                   o_stride_s % 4 == 0 && o_stride_h % 4 == 0 && ok_stride_s % 4 == 0 &&
+                   ok_stride_h % 4 == 0,
+               "zero_order_compensation: rows must be aligned");
+  VEDA_REQUIRE(2 * c_stride_s < (1 << 24), "zero_order_compensation: summary stride too large");
+  const int64_t items = n_heads * n_q_tiles;
+  if (items == 0) return VEDA_OK;
+  VEDA_REQUIRE(n_k_tiles >= 1 && n_k_tiles <= kMaxBlocks,
+               "zero_order_compensation: n_k_tiles %lld outside [1, %d]", (long long)n_k_tiles,
+               kMaxBlocks);
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(kc);
+  p.v = static_cast<const uint16_t*>(vc);
+  p.qs = q_stride_s; p.qh = q_stride_h;
+  p.ks = c_stride_s; p.kh = c_stride_h;
+  p.vs = c_stride_s; p.vh = c_stride_h;
+  p.n_heads = n_heads; p.n_q_tiles = n_q_tiles; p.n_k_tiles = n_k_tiles;
+  p.valid_count = valid_count;
+  p.q_rows = n_q_tiles * kTile;
+  p.scale_log2 = (float)((double)scale * 1.4426950408889634);
+  p.out = static_cast<uint16_t*>(out);
+  p.os = o_stride_s; p.oh = o_stride_h;
+  p.keep = keep;
+  p.o_kept = static_cast<const uint16_t*>(o_kept);
+  p.oks = ok_stride_s; p.okh = ok_stride_h;
+  p.lse_kept = lse_kept; p.lk_h = lse_stride_h; p.lk_s = lse_stride_s;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hfwd_kernel<kVirtual, kNoHeat, true><<<(unsigned)items, kThreads, 0, s>>>(p);
+  return check_launch("veda_zero_order_compensation");
 }

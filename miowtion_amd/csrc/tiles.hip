@@ -254,6 +254,64 @@ __global__ void gather_lse_kernel(const float* __restrict__ lse, int64_t rows,
   out[i] = v;
 }
 
+// Tile summaries for the zero-order compensation: per (key tile, head) the
+// mean of K over the tile's real rows (divided by max(count, 1)) and the
+// sum of V over them, both rounded to bf16 (the summaries of
+// miowtion/kernels/compensation_triton.py:80-99; real rows are the first
+// valid_count[t] slots). Workgroup = (tile, 4 heads): lane (head, 16-byte
+// chunk), wave = 32 slots; fp32 sums, reduced across waves through LDS.
+__global__ void __launch_bounds__(256) summary_kernel(
+    const uint16_t* __restrict__ k, int64_t ks, int64_t kh, const uint16_t* __restrict__ v,
+    int64_t vs, int64_t vh, const int32_t* __restrict__ valid_count, int64_t n_heads,
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t cs, int64_t ch) {
+  constexpr int kChunks = 16;  // D = 128
+  const int tile = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t head = (int64_t)blockIdx.y * 4 + lane / kChunks;
+  const int chunk = lane % kChunks;
+  const bool head_ok = head < n_heads;
+  const int count = min(max(valid_count[tile], 0), kTile);
+  float sk[8], sv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sk[e] = sv[e] = 0.f;
+  const int first = wave * kSlotsPerWave, last = min(first + kSlotsPerWave, count);
+  for (int i = first; i < last && head_ok; ++i) {
+    const int64_t row = (int64_t)tile * kTile + i;
+    const Row8 a = load_row8(k + row * ks + head * kh + chunk * 8);
+    const Row8 b = load_row8(v + row * vs + head * vh + chunk * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sk[e] += elem(a, e);
+      sv[e] += elem(b, e);
+    }
+  }
+  __shared__ float red[2][kWaves][64][8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    red[0][wave][lane][e] = sk[e];
+    red[1][wave][lane][e] = sv[e];
+  }
+  __syncthreads();
+  if (wave != 0 || !head_ok) return;
+  const float denom = (float)(count > 1 ? count : 1);
+  Row8 ok = {{0u, 0u, 0u, 0u}}, ov = {{0u, 0u, 0u, 0u}};
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      a0 += red[0][w][lane][e];
+      a1 += red[0][w][lane][e + 1];
+      b0 += red[1][w][lane][e];
+      b1 += red[1][w][lane][e + 1];
+    }
+    ok.w[e >> 1] = pack_bf16x2(a0 / denom, a1 / denom);
+    ov.w[e >> 1] = pack_bf16x2(b0, b1);
+  }
+  store_row8(kc + (int64_t)tile * cs + head * ch + chunk * 8, ok);
+  store_row8(vc + (int64_t)tile * cs + head * ch + chunk * 8, ov);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -346,4 +404,25 @@ extern "C" int veda_gather_lse(const float* lse, int64_t lse_rows, int64_t lse_h
       lse, lse_rows, lse_heads, lse_stride_s, lse_stride_h, gather_index, slot_valid, n_slots,
       heads, n_heads, out);
   return check_launch("veda_gather_lse");
+}
+
+extern "C" int veda_tile_summaries(const void* k, int64_t k_stride_s, int64_t k_stride_h,
+                                   const void* v, int64_t v_stride_s, int64_t v_stride_h,
+                                   const int32_t* valid_count, int64_t n_tiles, int64_t n_heads,
+                                   int64_t head_dim, void* kc, void* vc, int64_t c_stride_s,
+                                   int64_t c_stride_h, void* stream) {
+  VEDA_REQUIRE(head_dim == 128, "tile_summaries: head_dim must be 128, got %lld",
+               (long long)head_dim);
+  VEDA_REQUIRE(n_tiles >= 0 && n_heads >= 0, "tile_summaries: negative size");
+  VEDA_REQUIRE(aligned16(k) && aligned16(v) && aligned16(kc) && aligned16(vc) &&
+                   k_stride_s % 8 == 0 && k_stride_h % 8 == 0 && v_stride_s % 8 == 0 &&
+                   v_stride_h % 8 == 0 && c_stride_s % 8 == 0 && c_stride_h % 8 == 0,
+               "tile_summaries: rows must be 16-byte aligned");
+  if (n_tiles == 0 || n_heads == 0) return VEDA_OK;
+  dim3 grid((unsigned)n_tiles, (unsigned)((n_heads + 3) / 4));
+  summary_kernel<<<grid, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(k), k_stride_s, k_stride_h, static_cast<const uint16_t*>(v),
+      v_stride_s, v_stride_h, valid_count, n_heads, static_cast<uint16_t*>(kc),
+      static_cast<uint16_t*>(vc), c_stride_s, c_stride_h);
+  return check_launch("veda_tile_summaries");
 }

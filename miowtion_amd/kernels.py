@@ -168,3 +168,43 @@ def dense_heat(q: torch.Tensor, k: torch.Tensor, layout: tiling.TileLayout,
     """
     res = ops.dense_heat(q, k, v, layout.valid_count, q_tiles, reduce)
     return res[0], res[1], (res[2] if v is not None else None)
+
+
+def tile_summaries(k: torch.Tensor, v: torch.Tensor, layout: tiling.TileLayout):
+    """(kc, vc) [n, H', D] bf16: per key tile the mean of K and the sum of V
+    over its real rows (compensation_triton.py:150-170)."""
+    kc, vc = ops.tile_summaries(k, v, layout.valid_count)
+    return kc, vc
+
+
+def zero_order_compensation(o_kept: torch.Tensor, lse_kept: torch.Tensor, q: torch.Tensor,
+                            k: torch.Tensor, v: torch.Tensor, block_mask: torch.Tensor,
+                            layout: tiling.TileLayout) -> torch.Tensor:
+    """Adds the zero-order term of every dropped key tile to a block-sparse
+    output (miowtion/veda/attention.py:591-689; the arithmetic of
+    compensation_triton.compensate, :173-225): a dropped tile is one virtual
+    key at its centroid carrying the sum of its values, weighted by its real
+    row count.
+
+    Args:
+        o_kept: [R * 128, H', D] bf16 block-sparse output over the kept blocks.
+        lse_kept: [H', R * 128] fp32 natural-log LSE over the kept blocks.
+        q: [R * 128, H', D] bf16 query tiles; k, v: [N, H', D] bf16 key tiles.
+        block_mask: [H', R, n] bool, True where the block was kept.
+        layout: Tile layout (real rows of every key tile).
+
+    Returns:
+        [R * 128, H', D] bf16.
+    """
+    kc, vc = tile_summaries(k, v, layout)
+    return ops.zero_order_compensation(o_kept, lse_kept, q, kc, vc, block_mask,
+                                       layout.valid_count)
+
+
+def compensated_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          block_mask: torch.Tensor, layout: tiling.TileLayout) -> torch.Tensor:
+    """Block-sparse attention over the kept blocks plus the zero-order term
+    of the dropped ones (compensation_triton.attention, :228-258)."""
+    kept = block_mask & layout.kv_ok[None, None, :]
+    o_kept, lse = block_sparse_attention(q, k, v, kept, layout, return_lse=True)
+    return zero_order_compensation(o_kept, lse, q, k, v, kept, layout)

@@ -405,6 +405,75 @@ def _(q, k, v, valid_count, q_tiles, reduce, workspace_bytes=HEAT_WORKSPACE_BYTE
     return res
 
 
+# Zero-order compensation (miowtion/veda/attention.py:591-689,
+# miowtion/kernels/compensation_triton.py:80-258)
+
+
+@torch.library.custom_op('veda::tile_summaries', mutates_args=())
+def tile_summaries(k: torch.Tensor, v: torch.Tensor, valid_count: torch.Tensor) -> list[torch.Tensor]:
+    """[kc, vc], both [n, H', D] bf16: mean of K and sum of V over each key
+    tile's real rows (compensation_triton.py:80-99)."""
+    _require_gpu(k, v, valid_count)
+    _check_rows('k', k)
+    _check_rows('v', v)
+    if k.shape != v.shape or k.shape[-1] != 128 or k.shape[0] % TILE:
+        raise ValueError("tile_summaries needs equal [n * 128, H', 128] k and v")
+    n = k.shape[0] // TILE
+    if valid_count.numel() != n or valid_count.dtype != torch.int32:
+        raise ValueError(f'valid_count must be int32 [{n}]')
+    kc = k.new_empty(n, k.shape[1], k.shape[2])
+    vc = torch.empty_like(kc)
+    _native.call('veda_tile_summaries', k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(),
+                 v.stride(0), v.stride(1), valid_count.contiguous().data_ptr(), n, k.shape[1],
+                 k.shape[2], kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
+                 _stream(k))
+    return [kc, vc]
+
+
+@tile_summaries.register_fake
+def _(k, v, valid_count):
+    kc = k.new_empty(k.shape[0] // TILE, k.shape[1], k.shape[2])
+    return [kc, torch.empty_like(kc)]
+
+
+@torch.library.custom_op('veda::zero_order_compensation', mutates_args=())
+def zero_order_compensation(o_kept: torch.Tensor, lse_kept: torch.Tensor, q: torch.Tensor,
+                            kc: torch.Tensor, vc: torch.Tensor, block_mask: torch.Tensor,
+                            valid_count: torch.Tensor) -> torch.Tensor:
+    """(o_kept + sum over dropped tiles of p vc) / (1 + sum of p B), p =
+    exp(q . kc / sqrt(D) - lse_kept); shapes as the reference's compensate()."""
+    _require_gpu(o_kept, lse_kept, q, kc, vc, block_mask, valid_count)
+    for name, t in (('o_kept', o_kept), ('q', q), ('kc', kc), ('vc', vc)):
+        _check_rows(name, t)
+    rows, heads, d = o_kept.shape
+    if q.shape != o_kept.shape or d != 128 or rows % TILE:
+        raise ValueError(f'q is {tuple(q.shape)}, o_kept {tuple(o_kept.shape)}; need equal '
+                         "[R * 128, H', 128]")
+    n = kc.shape[0]
+    if vc.shape != kc.shape or kc.shape[1:] != (heads, d):
+        raise ValueError(f"kc / vc must be [n, {heads}, {d}]")
+    if lse_kept.dtype != torch.float32 or tuple(lse_kept.shape) != (heads, rows):
+        raise ValueError(f'lse_kept must be fp32 [{heads}, {rows}]')
+    if block_mask.dtype != torch.bool or tuple(block_mask.shape) != (heads, rows // TILE, n):
+        raise ValueError(f'block_mask must be bool [{heads}, {rows // TILE}, {n}]')
+    if valid_count.numel() != n or valid_count.dtype != torch.int32:
+        raise ValueError(f'valid_count must be int32 [{n}]')
+    out = torch.empty_like(o_kept, memory_format=torch.contiguous_format)
+    keep = block_mask.contiguous()
+    _native.call('veda_zero_order_compensation', o_kept.data_ptr(), o_kept.stride(0),
+                 o_kept.stride(1), lse_kept.data_ptr(), lse_kept.stride(0), lse_kept.stride(1),
+                 q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(),
+                 kc.stride(0), kc.stride(1), keep.data_ptr(), valid_count.contiguous().data_ptr(),
+                 heads, d, rows // TILE, n, 1.0 / math.sqrt(d), out.data_ptr(), out.stride(0),
+                 out.stride(1), _stream(q))
+    return out
+
+
+@zero_order_compensation.register_fake
+def _(o_kept, lse_kept, q, kc, vc, block_mask, valid_count):
+    return torch.empty_like(o_kept)
+
+
 # --------------------------------------------------------------------------
 # predictor (miowtion/veda/predictor.py:251-338)
 

@@ -6,6 +6,7 @@ Restates:
   * _math_attention / dense_attention (math backend)
                             -> `miowtion/h3/attention.py:18-25,80-102`
   * teacher_heat_reference  -> `miowtion/veda/heatmap.py:36-99`
+  * zero_order_compensation -> `miowtion/veda/attention.py:591-689`
 
 The reference materialises [H', N, N]; this restatement does the same math
 per head and per chunk of query rows so that C2-sized heads fit in memory.
@@ -99,3 +100,48 @@ def teacher_heat(q, k, lse, lay: Layout, q_tiles, reduce='sum', score_dtype=torc
                 p = p.masked_fill(~row_ok[:, None], 0.0)
                 heat[h, ri] = p.sum(0)
     return heat
+
+
+def tile_summaries(k, v, valid_count, dtype=torch.float32):
+    """Per key tile and head: mean of K over its real rows (sum / max(count,
+    1)) and sum of V over them, [n, H', D] in `dtype`
+    (compensation_triton.py:80-99 stores bf16; attention.py:654-663 fp32)."""
+    n = valid_count.numel()
+    H, D = k.shape[1], k.shape[2]
+    real = (torch.arange(TILE)[None, :] < valid_count[:, None]).reshape(-1)[:, None, None]
+    ks = (k.float() * real).view(n, TILE, H, D).sum(1)
+    vs = (v.float() * real).view(n, TILE, H, D).sum(1)
+    counts = valid_count.float().clamp(min=1.0)
+    return (ks / counts[:, None, None]).to(dtype), vs.to(dtype)
+
+
+def zero_order_compensation(o_kept, lse_kept, q, k, v, block_mask, valid_count,
+                            summary_dtype=torch.float32):
+    """attention.py:591-689: every dropped key tile j (mask False, at least
+    one real row) stands for one virtual key mean_j(k) with value sum_j(v)
+    and weight B_j = its real row count; with the reference lse_kept (0 for
+    a row that kept nothing) the kept denominator is 1, so
+
+        out = (o_kept + sum_j p_j sum_j(v)) / (1 + sum_j p_j B_j),
+        p_j = exp(q . mean_j(k) / sqrt(D) - lse_kept).
+
+    summary_dtype=torch.bfloat16 rounds the summaries as the reference's
+    Triton kernel does (its one deliberate numeric difference)."""
+    Rq, H, D = q.shape
+    n = valid_count.numel()
+    scale = 1.0 / math.sqrt(D)
+    kc, vc = tile_summaries(k, v, valid_count, summary_dtype)
+    kc, vc = kc.float(), vc.float()
+    counts = valid_count.float()
+    out = torch.empty(Rq, H, D, dtype=torch.float32)
+    rows = torch.arange(Rq) // TILE
+    for h in range(H):
+        drop = (~block_mask[h][rows]) & (valid_count > 0)[None, :]      # [Rq, n]
+        ref = lse_kept[h]
+        ref = torch.where(torch.isfinite(ref), ref, torch.zeros_like(ref))
+        s = (q[:, h].float() @ kc[:, h].T) * scale
+        p = torch.exp(s - ref[:, None]) * drop.float()
+        num = p @ vc[:, h]
+        den = p @ counts
+        out[:, h] = (o_kept[:, h].float() + num) / (1.0 + den)[:, None]
+    return out.to(o_kept.dtype)
