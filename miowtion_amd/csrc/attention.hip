@@ -682,6 +682,278 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Sparse forward, two workgroups per CU.
+//
+// Workgroup = one (head, query tile), 4 waves; wave w owns query rows
+// 32 w .. 32 w + 31 and all 64 keys of every step (two 32-key sub-blocks,
+// A = keys 0..31, B = keys 32..63 of the step), so a wave's rows are
+// complete at the end and no key halves are merged. The ring is two K + V
+// slots (64 KB) with one step in flight, the step list 16-bit (key tile,
+// half, full-list flag) entries with a byte table of valid counts: 74 KB of
+// LDS, so two workgroups share a CU. Their waves are not tied by a barrier,
+// so the two waves of a SIMD drift apart and fill each other's stalls.
+
+constexpr int kThreads2 = 256;
+constexpr uint16_t kVoidStep = 0xFFFF;  // list entry outside [0, n_k): no valid key
+
+// Per-lane byte offsets of this wave's eight 1 KB segments of a step
+// (segments 4 w + u, u = 0..3, of K and of V: rows 4 seg + l / 16), and of
+// their redirect (rows l / 16) for segments wholly past the valid count.
+struct SDma {
+  uint32_t k[4], v[4], k_skip[4], v_skip[4];
+};
+
+__device__ __forceinline__ SDma sdma_offsets(int64_t ks, int64_t vs, int wave, int lane) {
+  SDma d;
+  const int lr = lane >> 4, pc = lane & 15;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int row = 4 * (4 * wave + u) + lr;
+    const int kc = (pc ^ (row & 15)) << 3, vc = (pc ^ ((row & 3) << 2)) << 3;
+    d.k[u] = (uint32_t)((row * ks + kc) * 2);
+    d.v[u] = (uint32_t)((row * vs + vc) * 2);
+    d.k_skip[u] = (uint32_t)((lr * ks + kc) * 2);
+    d.v_skip[u] = (uint32_t)((lr * vs + vc) * 2);
+  }
+  return d;
+}
+
+// Scores of one 32-key sub-block, masked past `lim` keys of it (lim >= 32: none).
+__device__ __forceinline__ f32x16 sub_scores(const lds_u8* slot, const HFrag& f,
+                                             const WaveState& w, int lim, int hi) {
+  u32x4 kf[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    kf[k] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(slot + f.k[k]);
+  f32x16 s;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) s[e] = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[k]), w.qf[k], s, 0, 0, 0);
+  if (lim < 32) {
+    const int l = lim - 4 * hi;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (8 * (e >> 2) + (e & 3) >= l) s[e] = -INFINITY;
+  }
+  return s;
+}
+
+__device__ __forceinline__ void sub_pv(const lds_u8* slot, const HFrag& f, const u32x4 (&pk)[2],
+                                       WaveState& w) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const lds_u8* vs = slot + kk * 16 * 256;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + f.v[dt]));
+      const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + 8 * 256 + f.v[dt]));
+      const bf16x8 a =
+          __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
+      w.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pk[kk]), w.o[dt], 0, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void pack_probs(const float (&ps)[16], u32x4 (&pk)[2]) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) pk[kk][m] = pack_bf16x2(ps[8 * kk + 2 * m], ps[8 * kk + 2 * m + 1]);
+}
+
+// One step of one wave over the step's vch valid keys (sub-block B only
+// when vch > 32): the same online softmax as hstep, over 64 keys.
+template <bool TWO>
+__device__ __forceinline__ void sstep(const lds_u8* slot, const HFrag& fa, const HFrag& fb,
+                                      float c, int vch, int hi, WaveState& w) {
+  const f32x16 sa = sub_scores(slot, fa, w, vch, hi);
+  f32x16 sb;
+  if (TWO) sb = sub_scores(slot, fb, w, vch - 32, hi);
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sa[e]);
+  if (TWO) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sb[e]);
+  }
+  mloc = half_swap_max(mloc) * c;
+  const float m_new = mloc > w.m_run + kRescaleSlack ? mloc : w.m_run;
+  const float mu = m_new == -INFINITY ? 0.f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(w.m_run - mu);
+  w.m_run = m_new;
+  float pa[16], pb[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) pa[e] = __builtin_amdgcn_exp2f(fmaf(sa[e], c, -mu));
+  float l4[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) l4[g] = (pa[4 * g] + pa[4 * g + 1]) + (pa[4 * g + 2] + pa[4 * g + 3]);
+  float lsum = (l4[0] + l4[1]) + (l4[2] + l4[3]);
+  if (TWO) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) pb[e] = __builtin_amdgcn_exp2f(fmaf(sb[e], c, -mu));
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      l4[g] = (pb[4 * g] + pb[4 * g + 1]) + (pb[4 * g + 2] + pb[4 * g + 3]);
+    lsum += (l4[0] + l4[1]) + (l4[2] + l4[3]);
+  }
+  w.l_run = fmaf(w.l_run, alpha, lsum);
+  u32x4 ka[2], kb[2];
+  pack_probs(pa, ka);
+  if (TWO) pack_probs(pb, kb);
+  if (__any(alpha != 1.f)) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) w.o[dt][e] *= alpha;
+  }
+  sub_pv(slot, fa, ka, w);
+  if (TWO) sub_pv(slot, fb, kb, w);
+}
+
+__global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[2][kSlotBytes];
+  __shared__ uint16_t steps[2 * kMaxBlocks];
+  __shared__ uint8_t tvc[kMaxBlocks];
+  __shared__ int32_t step_total;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int li = lane & 31, hi = lane >> 5;
+  const int64_t item = blockIdx.x;
+  const int64_t head = item / p.n_q_tiles;
+  const int64_t r = item % p.n_q_tiles;
+  const int64_t qrow = r * kTile + 32 * wave + li;
+
+  // Step list: full-list tiles as two unmasked halves, then the first
+  // halves of the partial-list tiles, then their second halves (those with
+  // more than 64 valid keys), each in list order (ballot-ranked, so the
+  // summation order is deterministic); valid counts in a byte table.
+  const int nk = (int)p.n_k_tiles;
+  for (int j = tid; j < nk; j += kThreads2) tvc[j] = (uint8_t)min(max(p.valid_count[j], 0), kTile);
+  const int64_t li_ = head * p.n_q_tiles + r;
+  const int ld = (int)p.list_ld;
+  const int nf = min(max(p.full_cnt[li_], 0), min(ld, kMaxBlocks));
+  const int np = min(max(p.part_cnt[li_], 0), min(ld, kMaxBlocks - nf));
+  const int32_t* fl = p.full_idx + li_ * p.list_ld;
+  const int32_t* pl = p.part_idx + li_ * p.list_ld;
+  for (int i = tid; i < nf; i += kThreads2) {
+    const int32_t j = fl[i];
+    const bool ok = j >= 0 && j < nk;
+    steps[2 * i] = ok ? (uint16_t)((j << 2) | 1) : kVoidStep;
+    steps[2 * i + 1] = ok ? (uint16_t)((j << 2) | 3) : kVoidStep;
+  }
+  if (wave == 0) {
+    int h1 = 0;
+    for (int i0 = 0; i0 < np; i0 += 64) {
+      const int i = i0 + lane;
+      int vc = 0;
+      int32_t j = -1;
+      if (i < np) {
+        j = pl[i];
+        const bool ok = j >= 0 && j < nk;
+        if (ok) vc = min(max(p.valid_count[j], 0), kTile);
+        steps[2 * nf + i] = ok ? (uint16_t)(j << 2) : kVoidStep;
+      }
+      const bool two = i < np && vc > kHalf;
+      const uint64_t bal = __ballot(two);
+      const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+      if (two) steps[2 * nf + np + h1 + rank] = (uint16_t)((j << 2) | 2);
+      h1 += __builtin_popcountll(bal);
+    }
+    if (lane == 0) step_total = 2 * nf + np + h1;
+  }
+
+  WaveState w;
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    w.qf[s] = as_bf16x8(ld16(p.q + qrow * p.qs + head * p.qh + 16 * s + 8 * hi));
+#pragma unroll
+  for (int s = 0; s < 8; ++s) asm volatile("" : : "v"(w.qf[s]));
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) w.o[dt][e] = 0.f;
+  w.m_run = -INFINITY;
+  w.l_run = 0.f;
+  __syncthreads();  // step list, valid counts and step count ready
+  const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
+
+  // (first key row, valid keys) of step u
+  auto decode = [&](int u, int64_t& row0, int& vch) {
+    const int e = __builtin_amdgcn_readfirstlane(steps[u]);
+    if (e == kVoidStep) {
+      row0 = 0;
+      vch = 0;
+      return;
+    }
+    const int j = e >> 2, half = (e >> 1) & 1, full = e & 1;
+    const int vc = full ? kTile : __builtin_amdgcn_readfirstlane(tvc[j]);
+    row0 = (int64_t)j * kTile + half * kHalf;
+    vch = half ? vc - kHalf : min(vc, kHalf);
+  };
+  const uint16_t* kbase = p.k + head * p.kh;
+  const uint16_t* vbase = p.v + head * p.vh;
+  const float c = p.scale_log2;
+  const SDma dma = sdma_offsets(p.ks, p.vs, wave, lane);
+  const HFrag fa = hfrag_offsets(0, lane), fb = hfrag_offsets(1, lane);
+  auto load_step = [&](int u, lds_u8* slot) {
+    int64_t row0;
+    int vch;
+    decode(u, row0, vch);
+    const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
+    const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
+#pragma unroll
+    for (int u4 = 0; u4 < 4; ++u4) {
+      const int seg = 4 * wave + u4;
+      const bool live = 4 * seg < vch;
+      dma16(kb, live ? dma.k[u4] : dma.k_skip[u4], slot + seg * 1024);
+      dma16(vb, live ? dma.v[u4] : dma.v_skip[u4], slot + kHalfBytes + seg * 1024);
+    }
+  };
+  lds_u8* s0 = (lds_u8*)ring[0];
+  lds_u8* s1 = (lds_u8*)ring[1];
+  // Step u: wait for its own loads (the only ones in flight), barrier (all
+  // waves' loads of step u are in LDS and all are done reading the other
+  // slot), issue step u + 1 into the other slot, compute step u.
+  auto run = [&](int u, lds_u8* cur, lds_u8* nxt) {
+    VEDA_WAIT_VM(0);
+    __builtin_amdgcn_s_barrier();
+    if (u + 1 < n_steps) load_step(u + 1, nxt);
+    int64_t row0;
+    int vch;
+    decode(u, row0, vch);
+    if (vch > 32) sstep<true>(cur, fa, fb, c, vch, hi, w);
+    else if (vch > 0) sstep<false>(cur, fa, fb, c, vch, hi, w);
+  };
+  if (n_steps > 0) load_step(0, s0);
+  for (int u = 0; u < n_steps; u += 2) {
+    run(u, s0, s1);
+    if (u + 1 >= n_steps) break;
+    run(u + 1, s1, s0);
+  }
+
+  const float l = half_swap_sum(w.l_run);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  uint16_t* orow = p.out + qrow * p.os + head * p.oh;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int e = 4 * g;
+      const int d = 32 * dt + 8 * g + 4 * hi;
+      uint32_t w0 = pack_bf16x2(w.o[dt][e] * inv, w.o[dt][e + 1] * inv);
+      uint32_t w1 = pack_bf16x2(w.o[dt][e + 2] * inv, w.o[dt][e + 3] * inv);
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<u32x2*>(orow + d) = u32x2{w0, w1};
+    }
+  if (p.lse != nullptr && hi == 0)
+    p.lse[head * p.lse_sh + qrow * p.lse_ss] =
+        l > 0.f ? (w.m_run + __log2f(l)) * kLn2 : -INFINITY;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -733,7 +1005,7 @@ extern "C" int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t 
   p.os = o_stride_s; p.oh = o_stride_h;
   p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hfwd_kernel<kLists, kNoHeat, true><<<(unsigned)items, kThreads, 0, s>>>(p);
+  sfwd_kernel<<<(unsigned)items, kThreads2, 0, s>>>(p);
   return check_launch("veda_block_sparse_fwd");
 }
 
