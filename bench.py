@@ -399,7 +399,7 @@ def main() -> int:
         'dense': dense,
         'roofline': {'bound': 'mfma', 'achieved': round(achieved, 2), 'peak': PEAK_BF16_TFLOPS,
                      'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_BF16_TFLOPS, 4),
-                     'traffic': _traffic(), 'kernel': 'hfwd_kernel<kLists, kNoHeat, true> (veda_block_sparse_fwd)',
+                     'traffic': _traffic(), 'kernel': 'sfwd_kernel (veda_block_sparse_fwd)',
                      'avg_launch_ms': round(k_avg, 4),
                      'achieved_on_executed_flop': round(exec_flop / (k_avg * 1e-3) / 1e12, 2)},
         'cpu_baseline': cpu,
