@@ -282,6 +282,47 @@ int veda_zero_order_compensation(const void* o_kept, int64_t ok_stride_s,
                                  int64_t o_stride_h, void* stream);
 
 /*
+ * Block-sparse attention backward: the gradients of veda_block_sparse_fwd
+ * (FA4's backward with the Q-direction lists, reached through
+ * miowtion/kernels/fa4.py:340-373 -> fa4_sm8x/interface.py:3722-3790
+ * FlashAttnFunc.backward -> :2099 _flash_attn_bwd; the block-sparse main
+ * loop is fa4_sm8x/flash_bwd.py:1261-1340). With P the forward's softmax
+ * over the kept key tiles' valid keys,
+ *   D = rowsum(dout * out) - dlse,   dS = P * (dout V^T - D)
+ *   dq = dS K * scale,  dk = dS^T Q * scale,  dv = P^T dout.
+ * q, out, dout, dq: bf16 [n_q_tiles * 128, n_heads, 128]; k, v, dk, dv: bf16
+ * [n_k_tiles * 128, n_heads, 128] (strides in elements, last dim 1). lse:
+ * the forward's natural-log LSE, lse[h * lse_stride_h + row *
+ * lse_stride_s]; dlse: its gradient in the same form, or NULL.
+ * full_* / part_*: the forward lists (rows = query tiles, entries = key
+ * tiles, row stride list_ld); full_*_t / part_*_t: the transposed lists
+ * (rows = key tiles, entries = query tiles, row stride list_ld_t), as
+ * fa4.py:275-296 index_lists(transpose=True) builds them. Every row of
+ * dq, dk, dv is written (0 where no block reaches it). workspace: at least
+ * n_heads * n_q_tiles * 2048 bytes of device memory, 16-byte aligned
+ * (per-row statistics; contents on entry do not matter).
+ */
+int veda_block_sparse_bwd(const void* q, int64_t q_stride_s, int64_t q_stride_h,
+                          const void* k, int64_t k_stride_s, int64_t k_stride_h,
+                          const void* v, int64_t v_stride_s, int64_t v_stride_h,
+                          const void* out, int64_t o_stride_s, int64_t o_stride_h,
+                          const void* dout, int64_t do_stride_s, int64_t do_stride_h,
+                          const float* lse, int64_t lse_stride_h, int64_t lse_stride_s,
+                          const float* dlse, int64_t dlse_stride_h,
+                          int64_t dlse_stride_s, int64_t n_heads, int64_t head_dim,
+                          int64_t n_q_tiles, int64_t n_k_tiles,
+                          const int32_t* full_cnt, const int32_t* full_idx,
+                          const int32_t* part_cnt, const int32_t* part_idx,
+                          int64_t list_ld, const int32_t* full_cnt_t,
+                          const int32_t* full_idx_t, const int32_t* part_cnt_t,
+                          const int32_t* part_idx_t, int64_t list_ld_t,
+                          const int32_t* valid_count, float scale, void* dq,
+                          int64_t dq_stride_s, int64_t dq_stride_h, void* dk,
+                          int64_t dk_stride_s, int64_t dk_stride_h, void* dv,
+                          int64_t dv_stride_s, int64_t dv_stride_h, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
+/*
  * Predictor tile embedding, miowtion/veda/predictor.py:251-255:
  *   out[h', t, :] = feats[h', t, :] @ W[heads[h']] (+ feats[h', t, :n_out]
  *   when residual), fp32 accumulation.

@@ -41,6 +41,10 @@ SIGNATURES: dict[str, list] = {
     'veda_tile_summaries': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _P, _P, _I, _I, _P],
     'veda_zero_order_compensation': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _P, _I, _I, _P, _P,
                                      _I, _I, _I, _I, _F, _P, _I, _I, _P],
+    'veda_block_sparse_bwd': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _I,
+                              _P, _I, _I, _P, _I, _I, _I, _I, _I, _I,
+                              _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _F,
+                              _P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _P],
     'veda_predictor_embed': [_P, _I, _I, _I, _P, _C, _P, _I, _P, _I, _C, _P, _P],
     'veda_predictor_logits': [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _C, _P, _P],
 }

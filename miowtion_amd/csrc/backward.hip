@@ -1,0 +1,632 @@
+// Block-sparse flash-attention backward for gfx950 (head_dim 128, bf16
+// operands and gradients, fp32 accumulation): dQ, dK, dV of
+//   O = softmax(Q K^T * scale over the kept key tiles' valid keys) V
+// given dO and the forward's per-row log-sum-exp.
+//
+// Three kernels, none of them atomic: every gradient row is written by
+// exactly one workgroup, so the result does not depend on scheduling.
+//   bwd_stats_kernel  per 64-row step of every query tile: the LSE in log2
+//                     units (+inf for a row with no key, so its P is 0) and
+//                     D = rowsum(dO * O) - dLSE in fp32 (the LSE output's
+//                     gradient adds dLSE * P to dS), stored as a 1 KB record
+//                     [lse2 x 64 | D x 64 | 0 x 128] that one wave loads
+//                     into LDS with one DMA.
+//   dq_kernel         workgroup = (head, query tile), walking the forward
+//                     block lists (the key tiles of the row).
+//   dkv_kernel        workgroup = (head, key tile), walking the transposed
+//                     lists (the query tiles of the column).
+// Per pair of a 64-row and a 64-key half:
+//   P  = exp2(S * scale * log2(e) - lse2)   (0 past the key tile's valid count)
+//   dP = dO V^T,  dS = P * (dP - D)
+//   dQ += dS K * scale,  dK += dS^T Q * scale,  dV += P^T dO
+// dq_kernel forms the transposed products (S^T = K Q^T: a lane owns one
+// query row, as in the forward kernel), dkv_kernel the plain ones
+// (S = Q K^T: a lane owns one key), so that in each kernel P or dS goes from
+// the MFMA accumulators straight into the B operand of its own accumulation
+// (the MFMA contracts over k in any order, so lane half h supplies rows
+// 16 s + 4 h + {0..3, 8..11}, the order in which the accumulators hold them).
+//
+// LDS rows are 256 bytes (128 bf16). Logical 16-byte chunk c of row r sits at
+// position c ^ swz(r), swz(r) = 4 (r mod 4) + (r / 4 mod 4). Both read
+// patterns are free of bank conflicts with it: the 16-byte row reads of 16
+// consecutive rows (swz is a bijection on r mod 16) and the transposed 8-byte
+// reads (ds_read_b64_tr_b16) of 4 consecutive rows by 16 lanes, whose chunk
+// positions differ in bits 2-3. Tiles go from HBM into LDS with
+// global_load_lds_dwordx4 (the swizzle is applied by the choice of source
+// address), double-buffered: step u + 1 loads while step u computes.
+
+#include "veda_common.h"
+#include "veda_pipeline.h"
+
+namespace veda {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kMaxTiles = 2048;                  // tiles per list row (FA4's cap)
+constexpr int kRecFloats = 256;                  // stats record: 64 lse2, 64 D, 128 zero
+constexpr int kRecBytes = kRecFloats * 4;
+constexpr int kDqThreads = 512;
+constexpr int kDkvThreads = 256;
+constexpr int kSlot = 2 * kHalfBytes;            // K + V (dq) or Q + dO (dkv) of a step
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct BwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;
+  const uint16_t* dout;
+  int64_t qs, qh, ks, kh, vs, vh, os, oh, dos, doh;
+  const float* lse;
+  int64_t lse_sh, lse_ss;
+  const float* dlse;  // NULL: the LSE output carries no gradient
+  int64_t dlse_sh, dlse_ss;
+  int64_t n_heads, n_q_tiles, n_k_tiles;
+  // forward lists: row = (head, query tile), entries = key tiles
+  const int32_t* full_cnt;
+  const int32_t* full_idx;
+  const int32_t* part_cnt;
+  const int32_t* part_idx;
+  int64_t list_ld;
+  // transposed lists: row = (head, key tile), entries = query tiles
+  const int32_t* full_cnt_t;
+  const int32_t* full_idx_t;
+  const int32_t* part_cnt_t;
+  const int32_t* part_idx_t;
+  int64_t list_ld_t;
+  const int32_t* valid_count;
+  float scale, scale_log2;
+  float* stats;  // [H'][2 R] records
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  int64_t dqs, dqh, dks, dkh, dvs, dvh;
+};
+
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+__device__ __forceinline__ int clamp_vc(int32_t vc) { return min(max(vc, 0), kTile); }
+
+// Byte offset (from the step's first row) that lane `lane` of 1 KB segment
+// `seg` loads: row 4 seg + lane / 16, LDS position lane % 16, which holds
+// logical chunk (lane % 16) ^ swz(row).
+__device__ __forceinline__ uint32_t seg_offset(int seg, int lane, int64_t stride) {
+  const int row = 4 * seg + (lane >> 4), pc = lane & 15;
+  return (uint32_t)((row * stride + ((pc ^ swz(row)) << 3)) * 2);
+}
+
+// Per-lane LDS byte offsets of the fragment reads of a 64-row region.
+//   row[s]:  A fragment of rows li (+ 32 g), chunk 2 s + hi (16-byte read).
+//   tr[dt][e]: transposed read of rows 4 hi + i / 4 + 8 e (+ 16 kk + 32 g),
+//            head-dims 32 dt + 16 dh + 4 (i % 4) .. + 3 (i = lane % 16,
+//            dh = lane / 16 % 2): lane (dh, i) receives the 4 rows at
+//            head-dim 32 dt + 16 dh + i, i.e. row m = lane % 32 of A^T.
+// The +32 g rows, +16 kk rows (4096 B) and region offsets are added as
+// immediates: none of them changes swz.
+struct Frag {
+  uint32_t row[8];
+  uint32_t tr[4][2];
+};
+
+__device__ __forceinline__ Frag frag_offsets(int lane) {
+  Frag f;
+  const int li = lane & 31, hi = lane >> 5;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) f.row[s] = li * 256 + (((2 * s + hi) ^ swz(li)) << 4);
+  const int i = lane & 15, dh = (lane >> 4) & 1;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int r = 4 * hi + (i >> 2) + 8 * e;
+      const int c = 4 * dt + 2 * dh + ((i >> 1) & 1);
+      f.tr[dt][e] = r * 256 + ((c ^ swz(r)) << 4) + 8 * (i & 1);
+    }
+  return f;
+}
+
+__device__ __forceinline__ u32x4 lds16(const lds_u8* p) {
+  return *reinterpret_cast<const lds_u32x4*>(p);
+}
+
+// A^T fragment (32 head-dims x 16 rows) of rows kk * 16 of the region at `base`.
+__device__ __forceinline__ bf16x8 tr_frag(const lds_u8* base, const Frag& f, int dt, int kk) {
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + kk * 4096 + f.tr[dt][0]));
+  const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + kk * 4096 + f.tr[dt][1]));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// The 16 accumulator values of a lane as the two B-operand k-steps
+// (rows 16 kk + 4 hi + {0..3, 8..11}), bf16.
+__device__ __forceinline__ void pack_b(const float (&x)[16], u32x4 (&pk)[2]) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) pk[kk][m] = pack_bf16x2(x[8 * kk + 2 * m], x[8 * kk + 2 * m + 1]);
+}
+
+// Stores 4 consecutive head-dims (accumulator values e0 .. e0 + 3) as bf16.
+__device__ __forceinline__ void store4(uint16_t* row, int d, const f32x16& a, int e0, float mul) {
+  const uint32_t w0 = pack_bf16x2(a[e0] * mul, a[e0 + 1] * mul);
+  const uint32_t w1 = pack_bf16x2(a[e0 + 2] * mul, a[e0 + 3] * mul);
+  *reinterpret_cast<u32x2*>(row + d) = u32x2{w0, w1};
+}
+
+// Wave 0 of a workgroup: the steps (target << 1 | half) of the full list,
+// then of the partial list, in list order; halves(t) = how many 64-row
+// halves of target t are steps (0 drops the entry). Returns the count.
+template <class Halves>
+__device__ int build_steps(const int32_t* fl, int nf, const int32_t* pl, int np, int lane,
+                           uint16_t* steps, Halves halves) {
+  int n = 0;
+  const int total = nf + np;
+  for (int i0 = 0; i0 < total; i0 += 64) {
+    const int i = i0 + lane;
+    int t = 0, h = 0;
+    if (i < total) {
+      t = i < nf ? fl[i] : pl[i - nf];
+      h = halves(t);
+    }
+    const uint64_t b0 = __ballot(h >= 1), b1 = __ballot(h >= 2);
+    const int rank =
+        __builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0)) +
+        __builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0));
+    if (h >= 1) steps[n + rank] = (uint16_t)(t << 1);
+    if (h >= 2) steps[n + rank + 1] = (uint16_t)((t << 1) | 1);
+    n += __builtin_popcountll(b0) + __builtin_popcountll(b1);
+  }
+  return n;
+}
+
+// Clamped entry counts of list row `lr` (at most kMaxTiles together).
+__device__ __forceinline__ void list_counts(const int32_t* fc, const int32_t* pc, int64_t lr,
+                                            int64_t ld, int& nf, int& np) {
+  const int cap = (int)min(ld, (int64_t)kMaxTiles);
+  nf = min(max(fc[lr], 0), cap);
+  np = min(max(pc[lr], 0), min(cap, kMaxTiles - nf));
+}
+
+// ---------------------------------------------------------------------------
+// Row statistics. Block = one 64-row record; 16 lanes per row, each lane 8
+// head-dims.
+
+__global__ void __launch_bounds__(256) bwd_stats_kernel(BwdParams p) {
+  const int64_t rec = blockIdx.x;
+  const int64_t per_head = 2 * p.n_q_tiles;
+  const int64_t head = rec / per_head, st = rec % per_head;
+  const int tid = threadIdx.x, sub = tid & 15;
+  float* out = p.stats + rec * kRecFloats;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int rr = 16 * it + (tid >> 4);
+    const int64_t row = st * 64 + rr;
+    const u32x4 a = ld16(p.o + row * p.os + head * p.oh + 8 * sub);
+    const u32x4 b = ld16(p.dout + row * p.dos + head * p.doh + 8 * sub);
+    float acc = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      acc = fmaf(bf16_to_f32(a[m] & 0xffffu), bf16_to_f32(b[m] & 0xffffu), acc);
+      acc = fmaf(bf16_to_f32(a[m] >> 16), bf16_to_f32(b[m] >> 16), acc);
+    }
+    acc += __shfl_xor(acc, 8, 16);
+    acc += __shfl_xor(acc, 4, 16);
+    acc += __shfl_xor(acc, 2, 16);
+    acc += __shfl_xor(acc, 1, 16);
+    if (sub == 0) {
+      const float l = p.lse[head * p.lse_sh + row * p.lse_ss];
+      out[rr] = l == -INFINITY ? INFINITY : l * kLog2e;
+      out[64 + rr] = p.dlse != nullptr ? acc - p.dlse[head * p.dlse_sh + row * p.dlse_ss] : acc;
+    }
+  }
+  if (tid < 128) out[128 + tid] = 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// dQ. Workgroup = (head, query tile), 8 waves: wave w owns query rows
+// 32 (w % 4) .. + 31 (one per lane, as B = Q^T and dO^T fragments in
+// registers) and keys 32 (w / 4) .. + 31 of every 64-key step; the two key
+// halves keep separate dQ^T accumulators, summed through LDS at the end.
+// Per step and wave: S^T = K Q^T and dP^T = V dO^T (8 MFMAs each, A = K / V
+// rows from LDS), dS^T, then dQ^T += K^T dS^T (8 MFMAs, A = transposed K reads).
+
+__global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[2][kSlot];
+  __shared__ uint16_t steps[2 * kMaxTiles];
+  __shared__ uint8_t tvc[kMaxTiles];
+  __shared__ int32_t step_total;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int li = lane & 31, hi = lane >> 5;
+  const int qg = wave & 3, kh = wave >> 2;
+  const int64_t item = blockIdx.x;
+  const int64_t head = item / p.n_q_tiles, r = item % p.n_q_tiles;
+  const int64_t qrow = r * kTile + 32 * qg + li;
+  const int nk = (int)p.n_k_tiles;
+
+  for (int j = tid; j < nk; j += kDqThreads) tvc[j] = (uint8_t)clamp_vc(p.valid_count[j]);
+  if (wave == 0) {
+    const int64_t lr = head * p.n_q_tiles + r;
+    int nf, np;
+    list_counts(p.full_cnt, p.part_cnt, lr, p.list_ld, nf, np);
+    const int n = build_steps(p.full_idx + lr * p.list_ld, nf, p.part_idx + lr * p.list_ld, np,
+                              lane, steps, [&](int t) {
+                                if (t < 0 || t >= nk) return 0;
+                                const int vc = clamp_vc(p.valid_count[t]);
+                                return vc > kHalf ? 2 : vc > 0 ? 1 : 0;
+                              });
+    if (lane == 0) step_total = n;
+  }
+
+  bf16x8 qf[8], dof[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    qf[s] = as_bf16x8(ld16(p.q + qrow * p.qs + head * p.qh + 16 * s + 8 * hi));
+    dof[s] = as_bf16x8(ld16(p.dout + qrow * p.dos + head * p.doh + 16 * s + 8 * hi));
+  }
+  const float* rec = p.stats + (head * 2 * p.n_q_tiles + 2 * r + (qg >> 1)) * kRecFloats;
+  const float lse2 = rec[(32 * qg + li) & 63];
+  const float dq_d = rec[64 + ((32 * qg + li) & 63)];
+  f32x16 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
+  __syncthreads();  // step list and valid counts ready
+  const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
+
+  const uint16_t* kbase = p.k + head * p.kh;
+  const uint16_t* vbase = p.v + head * p.vh;
+  uint32_t koff[2], voff[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    koff[u] = seg_offset(2 * wave + u, lane, p.ks);
+    voff[u] = seg_offset(2 * wave + u, lane, p.vs);
+  }
+  const Frag f = frag_offsets(lane);
+  const uint32_t kb32 = 32 * kh * 256;  // this wave's keys inside a step
+  const float c = p.scale_log2;
+
+  auto load_step = [&](int u, lds_u8* slot) {
+    const int t = __builtin_amdgcn_readfirstlane(steps[u]);
+    const int64_t row0 = (int64_t)(t >> 1) * kTile + (t & 1) * kHalf;
+    const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
+    const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      dma16(kb, koff[s], slot + (2 * wave + s) * 1024);
+      dma16(vb, voff[s], slot + kHalfBytes + (2 * wave + s) * 1024);
+    }
+  };
+  auto compute = [&](int u, const lds_u8* slot) {
+    const int t = __builtin_amdgcn_readfirstlane(steps[u]);
+    const int vc = __builtin_amdgcn_readfirstlane((int)tvc[t >> 1]);
+    const int lim = (t & 1 ? vc - kHalf : min(vc, kHalf)) - 32 * kh;  // valid keys of this wave
+    if (lim <= 0) return;
+    const lds_u8* ks = slot + kb32;
+    const lds_u8* vs = slot + kHalfBytes + kb32;
+    f32x16 st, dp;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      st[e] = 0.f;
+      dp[e] = 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(ks + f.row[s])), qf[s], st, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(vs + f.row[s])), dof[s], dp, 0, 0, 0);
+    float ds[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float pr = __builtin_amdgcn_exp2f(fmaf(st[e], c, -lse2));
+      if (lim < 32 && 8 * (e >> 2) + 4 * hi + (e & 3) >= lim) pr = 0.f;
+      ds[e] = pr * (dp[e] - dq_d);
+    }
+    u32x4 pk[2];
+    pack_b(ds, pk);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag(ks, f, dt, kk), as_bf16x8(pk[kk]),
+                                                          acc[dt], 0, 0, 0);
+  };
+
+  lds_u8* s0 = (lds_u8*)ring[0];
+  lds_u8* s1 = (lds_u8*)ring[1];
+  // Step u: wait for this wave's loads (the only ones in flight), barrier
+  // (every wave's loads of step u are in LDS and every wave is done reading
+  // the other slot), issue step u + 1 into the other slot, compute step u.
+  auto run = [&](int u, lds_u8* cur, lds_u8* nxt) {
+    VEDA_WAIT_VM(0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");  // no LDS read of step u above the barrier
+    if (u + 1 < n_steps) load_step(u + 1, nxt);
+    compute(u, cur);
+  };
+  if (n_steps > 0) load_step(0, s0);
+  for (int u = 0; u < n_steps; u += 2) {
+    run(u, s0, s1);
+    if (u + 1 >= n_steps) break;
+    run(u + 1, s1, s0);
+  }
+
+  // Sum the two key halves: waves 4..7 park their accumulators in the ring.
+  __syncthreads();
+  lds_f32* buf = (lds_f32*)ring[0];
+  if (kh == 1) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) buf[(qg * 64 + dt * 16 + e) * 64 + lane] = acc[dt][e];
+  }
+  __syncthreads();
+  if (kh == 0) {
+    uint16_t* drow = p.dq + qrow * p.dqs + head * p.dqh;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[dt][e] += buf[(qg * 64 + dt * 16 + e) * 64 + lane];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) store4(drow, 32 * dt + 8 * g + 4 * hi, acc[dt], 4 * g, p.scale);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV. Workgroup = (head, key tile), 4 waves: wave w owns keys
+// 32 w .. + 31 of the tile (one per lane, as B = K^T and V^T fragments in
+// registers) and their dK^T, dV^T accumulators. Per 64-row query step and
+// 32-row half of it: S = Q K^T and dP = dO V^T (8 MFMAs each, A = Q / dO
+// rows from LDS), P and dS, then dV^T += dO^T P and dK^T += Q^T dS (8 MFMAs
+// each, A = transposed dO / Q reads). The step's lse2 and D come with it.
+
+__global__ void __launch_bounds__(kDkvThreads, 1) dkv_kernel(BwdParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[2][kSlot + kRecBytes];
+  __shared__ uint16_t steps[2 * kMaxTiles];
+  __shared__ int32_t step_total;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int li = lane & 31, hi = lane >> 5;
+  const int64_t item = blockIdx.x;
+  const int64_t head = item / p.n_k_tiles, j = item % p.n_k_tiles;
+  const int vc = __builtin_amdgcn_readfirstlane(clamp_vc(p.valid_count[j]));
+  const int64_t krow = j * kTile + 32 * wave + li;
+  const int nq = (int)p.n_q_tiles;
+
+  if (wave == 0) {
+    const int64_t lr = head * p.n_k_tiles + j;
+    int nf, np;
+    list_counts(p.full_cnt_t, p.part_cnt_t, lr, p.list_ld_t, nf, np);
+    const int n = build_steps(p.full_idx_t + lr * p.list_ld_t, nf,
+                              p.part_idx_t + lr * p.list_ld_t, np, lane, steps,
+                              [&](int t) { return (vc > 0 && t >= 0 && t < nq) ? 2 : 0; });
+    if (lane == 0) step_total = n;
+  }
+
+  bf16x8 kf[8], vf[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    kf[s] = as_bf16x8(ld16(p.k + krow * p.ks + head * p.kh + 16 * s + 8 * hi));
+    vf[s] = as_bf16x8(ld16(p.v + krow * p.vs + head * p.vh + 16 * s + 8 * hi));
+  }
+  f32x16 dk[4], dv[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      dk[dt][e] = 0.f;
+      dv[dt][e] = 0.f;
+    }
+  __syncthreads();
+  const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
+
+  const uint16_t* qbase = p.q + head * p.qh;
+  const uint16_t* dbase = p.dout + head * p.doh;
+  uint32_t qoff[4], doff[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    qoff[u] = seg_offset(4 * wave + u, lane, p.qs);
+    doff[u] = seg_offset(4 * wave + u, lane, p.dos);
+  }
+  const Frag f = frag_offsets(lane);
+  const float c = p.scale_log2;
+  const bool key_ok = 32 * wave + li < vc;
+  const bool wave_live = 32 * wave < vc;
+
+  auto load_step = [&](int u, lds_u8* slot) {
+    const int t = __builtin_amdgcn_readfirstlane(steps[u]);
+    const int64_t row0 = (int64_t)(t >> 1) * kTile + (t & 1) * kHalf;
+    const char* qb = reinterpret_cast<const char*>(qbase + row0 * p.qs);
+    const char* db = reinterpret_cast<const char*>(dbase + row0 * p.dos);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      dma16(qb, qoff[s], slot + (4 * wave + s) * 1024);
+      dma16(db, doff[s], slot + kHalfBytes + (4 * wave + s) * 1024);
+    }
+    if (wave == 0) {
+      const float* rec = p.stats + (head * 2 * p.n_q_tiles + t) * kRecFloats;
+      dma16(reinterpret_cast<const char*>(rec), (uint32_t)(lane * 16), slot + kSlot);
+    }
+  };
+  auto compute = [&](const lds_u8* slot) {
+    const lds_u8* qs = slot;
+    const lds_u8* ds_ = slot + kHalfBytes;
+    const lds_u8* sr = slot + kSlot;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const lds_u8* qq = qs + qt * 8192;
+      const lds_u8* dd = ds_ + qt * 8192;
+      f32x16 sv, dp;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        sv[e] = 0.f;
+        dp[e] = 0.f;
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(qq + f.row[s])), kf[s], sv, 0, 0, 0);
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(dd + f.row[s])), vf[s], dp, 0, 0, 0);
+      // rows 32 qt + 8 g + 4 hi + {0..3} of the step
+      float pr[16], dsv[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r0 = 32 * qt + 8 * g + 4 * hi;
+        const f32x4 l4 = *reinterpret_cast<const lds_f32x4*>(sr + 4 * r0);
+        const f32x4 d4 = *reinterpret_cast<const lds_f32x4*>(sr + 256 + 4 * r0);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int e = 4 * g + m;
+          float x = __builtin_amdgcn_exp2f(fmaf(sv[e], c, -l4[m]));
+          x = key_ok ? x : 0.f;
+          pr[e] = x;
+          dsv[e] = x * (dp[e] - d4[m]);
+        }
+      }
+      u32x4 pk[2], sk[2];
+      pack_b(pr, pk);
+      pack_b(dsv, sk);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+          dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag(dd, f, dt, kk), as_bf16x8(pk[kk]),
+                                                           dv[dt], 0, 0, 0);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+          dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag(qq, f, dt, kk), as_bf16x8(sk[kk]),
+                                                           dk[dt], 0, 0, 0);
+    }
+  };
+
+  lds_u8* s0 = (lds_u8*)ring[0];
+  lds_u8* s1 = (lds_u8*)ring[1];
+  auto run = [&](int u, lds_u8* cur, lds_u8* nxt) {
+    VEDA_WAIT_VM(0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");  // no LDS read of step u above the barrier
+    if (u + 1 < n_steps) load_step(u + 1, nxt);
+    if (wave_live) compute(cur);
+  };
+  if (n_steps > 0) load_step(0, s0);
+  for (int u = 0; u < n_steps; u += 2) {
+    run(u, s0, s1);
+    if (u + 1 >= n_steps) break;
+    run(u + 1, s1, s0);
+  }
+  VEDA_WAIT_VM(0);
+
+  uint16_t* krow_p = p.dk + krow * p.dks + head * p.dkh;
+  uint16_t* vrow_p = p.dv + krow * p.dvs + head * p.dvh;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * dt + 8 * g + 4 * hi;
+      store4(krow_p, d, dk[dt], 4 * g, p.scale);
+      store4(vrow_p, d, dv[dt], 4 * g, 1.f);
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+}  // namespace
+}  // namespace veda
+
+using namespace veda;
+
+extern "C" int veda_block_sparse_bwd(
+    const void* q, int64_t q_stride_s, int64_t q_stride_h, const void* k, int64_t k_stride_s,
+    int64_t k_stride_h, const void* v, int64_t v_stride_s, int64_t v_stride_h, const void* out,
+    int64_t o_stride_s, int64_t o_stride_h, const void* dout, int64_t do_stride_s,
+    int64_t do_stride_h, const float* lse, int64_t lse_stride_h, int64_t lse_stride_s,
+    const float* dlse, int64_t dlse_stride_h, int64_t dlse_stride_s, int64_t n_heads,
+    int64_t head_dim, int64_t n_q_tiles, int64_t n_k_tiles,
+    const int32_t* full_cnt, const int32_t* full_idx, const int32_t* part_cnt,
+    const int32_t* part_idx, int64_t list_ld, const int32_t* full_cnt_t,
+    const int32_t* full_idx_t, const int32_t* part_cnt_t, const int32_t* part_idx_t,
+    int64_t list_ld_t, const int32_t* valid_count, float scale, void* dq, int64_t dq_stride_s,
+    int64_t dq_stride_h, void* dk, int64_t dk_stride_s, int64_t dk_stride_h, void* dv,
+    int64_t dv_stride_s, int64_t dv_stride_h, void* workspace, int64_t workspace_bytes,
+    void* stream) {
+  VEDA_REQUIRE(head_dim == kD, "block_sparse_bwd: head_dim must be 128, got %lld",
+               (long long)head_dim);
+  VEDA_REQUIRE(n_heads >= 0 && n_q_tiles >= 0 && n_k_tiles >= 0, "block_sparse_bwd: negative size");
+  VEDA_REQUIRE(n_q_tiles <= kMaxTiles && n_k_tiles <= kMaxTiles,
+               "block_sparse_bwd: at most %d query and key tiles, got %lld and %lld", kMaxTiles,
+               (long long)n_q_tiles, (long long)n_k_tiles);
+  VEDA_REQUIRE(list_ld >= n_k_tiles && list_ld_t >= n_q_tiles,
+               "block_sparse_bwd: list rows must hold n_k_tiles (forward) and n_q_tiles "
+               "(transposed) entries");
+  VEDA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(dout) &&
+                   q_stride_s % 8 == 0 && q_stride_h % 8 == 0 && k_stride_s % 8 == 0 &&
+                   k_stride_h % 8 == 0 && v_stride_s % 8 == 0 && v_stride_h % 8 == 0 &&
+                   o_stride_s % 8 == 0 && o_stride_h % 8 == 0 && do_stride_s % 8 == 0 &&
+                   do_stride_h % 8 == 0,
+               "block_sparse_bwd: q, k, v, out, dout rows must be 16-byte aligned");
+  VEDA_REQUIRE(aligned8(dq) && aligned8(dk) && aligned8(dv) && dq_stride_s % 4 == 0 &&
+                   dq_stride_h % 4 == 0 && dk_stride_s % 4 == 0 && dk_stride_h % 4 == 0 &&
+                   dv_stride_s % 4 == 0 && dv_stride_h % 4 == 0,
+               "block_sparse_bwd: dq, dk, dv rows must be 8-byte aligned");
+  // the LDS loads address a 64-row step with 32-bit byte offsets
+  VEDA_REQUIRE(q_stride_s < (1 << 24) && k_stride_s < (1 << 24) && v_stride_s < (1 << 24) &&
+                   do_stride_s < (1 << 24),
+               "block_sparse_bwd: row stride too large");
+  const int64_t need = n_heads * 2 * n_q_tiles * kRecBytes;
+  VEDA_REQUIRE(aligned16(workspace) && workspace_bytes >= need,
+               "block_sparse_bwd: workspace needs %lld bytes (16-byte aligned), got %lld",
+               (long long)need, (long long)workspace_bytes);
+  BwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.o = static_cast<const uint16_t*>(out);
+  p.dout = static_cast<const uint16_t*>(dout);
+  p.qs = q_stride_s; p.qh = q_stride_h;
+  p.ks = k_stride_s; p.kh = k_stride_h;
+  p.vs = v_stride_s; p.vh = v_stride_h;
+  p.os = o_stride_s; p.oh = o_stride_h;
+  p.dos = do_stride_s; p.doh = do_stride_h;
+  p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
+  p.dlse = dlse; p.dlse_sh = dlse_stride_h; p.dlse_ss = dlse_stride_s;
+  p.n_heads = n_heads; p.n_q_tiles = n_q_tiles; p.n_k_tiles = n_k_tiles;
+  p.full_cnt = full_cnt; p.full_idx = full_idx; p.part_cnt = part_cnt; p.part_idx = part_idx;
+  p.list_ld = list_ld;
+  p.full_cnt_t = full_cnt_t; p.full_idx_t = full_idx_t;
+  p.part_cnt_t = part_cnt_t; p.part_idx_t = part_idx_t;
+  p.list_ld_t = list_ld_t;
+  p.valid_count = valid_count;
+  p.scale = scale;
+  p.scale_log2 = (float)((double)scale * 1.4426950408889634);
+  p.stats = static_cast<float*>(workspace);
+  p.dq = static_cast<uint16_t*>(dq);
+  p.dk = static_cast<uint16_t*>(dk);
+  p.dv = static_cast<uint16_t*>(dv);
+  p.dqs = dq_stride_s; p.dqh = dq_stride_h;
+  p.dks = dk_stride_s; p.dkh = dk_stride_h;
+  p.dvs = dv_stride_s; p.dvh = dv_stride_h;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t q_items = n_heads * n_q_tiles, k_items = n_heads * n_k_tiles;
+  if (q_items > 0) {
+    bwd_stats_kernel<<<(unsigned)(2 * q_items), 256, 0, s>>>(p);
+    if (int rc = check_launch("veda_block_sparse_bwd (stats)")) return rc;
+    dq_kernel<<<(unsigned)q_items, kDqThreads, 0, s>>>(p);
+    if (int rc = check_launch("veda_block_sparse_bwd (dq)")) return rc;
+  }
+  if (k_items > 0) {
+    dkv_kernel<<<(unsigned)k_items, kDkvThreads, 0, s>>>(p);
+    return check_launch("veda_block_sparse_bwd (dk, dv)");
+  }
+  return VEDA_OK;
+}

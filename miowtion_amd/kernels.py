@@ -6,7 +6,8 @@ signatures:
   pool_tiles                      miowtion/veda/predictor.py:82-130
   gather_lse                      miowtion/veda/attention.py:299-305
   index_lists                     miowtion/kernels/fa4.py:275-296
-  block_sparse_attention          miowtion/kernels/fa4.py:299-377
+  block_sparse_attention          miowtion/kernels/fa4.py:299-377 (and its
+                                  backward, fa4_sm8x/interface.py:2099)
   dense_attention                 miowtion/h3/attention.py:28-102
   teacher_heat                    miowtion/kernels/block_heat_triton.py:141-173
 
@@ -98,10 +99,57 @@ def gather_lse(lse: torch.Tensor, layout: tiling.TileLayout, heads: torch.Tensor
     return ops.gather_lse(lse, layout.gather_index, layout.slot_valid, heads)
 
 
-def index_lists(block_mask: torch.Tensor, layout: tiling.TileLayout) -> tuple[torch.Tensor, ...]:
-    """(partial_cnt, partial_idx, full_cnt, full_idx): cnt [1, H', R] and idx
-    [1, H', R, n] int32, members ascending then non-members ascending."""
-    return tuple(ops.index_lists(block_mask, layout.kv_ok, layout.full_tile))
+def index_lists(block_mask: torch.Tensor, layout: tiling.TileLayout,
+                transpose: bool = False) -> tuple[torch.Tensor, ...]:
+    """(partial_cnt, partial_idx, full_cnt, full_idx) (fa4.py:275-296): cnt
+    [1, H', rows] and idx [1, H', rows, cols] int32, members ascending then
+    non-members ascending.
+
+    transpose: the Q-direction lists of the backward (per key tile, its query
+    tiles; a key tile's members are all full or all partial, by its own
+    fullness). Needs the mask of all n_tiles query tiles.
+    """
+    if not transpose:
+        return tuple(ops.index_lists(block_mask, layout.kv_ok, layout.full_tile))
+    if block_mask.shape[1] != layout.n_tiles:
+        raise ValueError('transposed lists need the block mask of all query tiles')
+    mt = (block_mask & layout.kv_ok[None, None, :]).transpose(1, 2).contiguous()
+    ones = torch.ones(mt.shape[2], dtype=torch.bool, device=mt.device)
+    # with every column "full", each row's members land in the full list
+    empty_cnt, empty_idx, cnt, idx = ops.index_lists(mt, ones, ones)
+    full_row = layout.full_tile.to(mt.device)[None, None, :]
+    return (torch.where(full_row, empty_cnt, cnt),
+            torch.where(full_row[..., None], empty_idx, idx).contiguous(),
+            torch.where(full_row, cnt, empty_cnt),
+            torch.where(full_row[..., None], idx, empty_idx).contiguous())
+
+
+class _BlockSparseAttention(torch.autograd.Function):
+    """Block-sparse attention with gradients: the forward kernel, then the
+    backward kernels on the forward and the transposed block lists
+    (FlashAttnFunc, fa4_sm8x/interface.py:3641-3790, given
+    block_sparse_tensors_bwd as fa4.py:352-360 builds them). The LSE output
+    is differentiable too (its gradient enters through D)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, block_mask, layout):
+        lists = index_lists(block_mask, layout)
+        lists_t = index_lists(block_mask, layout, transpose=True)
+        out, lse = ops.block_sparse_fwd(q, k, v, *lists, layout.valid_count, True)
+        ctx.save_for_backward(q, k, v, out, lse, *lists, *lists_t, layout.valid_count)
+        ctx.set_materialize_grads(False)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        q, k, v, out, lse, *rest = ctx.saved_tensors
+        lists, lists_t, valid_count = rest[:4], rest[4:8], rest[8]
+        if dout is None:
+            dout = torch.zeros_like(out)
+        dq, dk, dv = ops.block_sparse_bwd(
+            q, k, v, out, dout.contiguous(), lse, None if dlse is None else dlse.contiguous(),
+            *lists, *lists_t, valid_count)
+        return dq, dk, dv, None, None
 
 
 def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -117,10 +165,17 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         return_lse: Also return the [H', R * 128] fp32 natural-log LSE.
 
     Returns:
-        [R * 128, H', D] bf16, or (out, lse).
+        [R * 128, H', D] bf16, or (out, lse). Differentiable in q, k, v
+        (and through the LSE) when they require grad.
+
+    Raises:
+        ValueError: If gradients are required for a subset of query tiles.
     """
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
-        raise NotImplementedError('the block-sparse backward is not part of this build')
+        if block_mask.shape[1] != layout.n_tiles:
+            raise ValueError('backward needs the block mask of all query tiles')
+        out, lse = _BlockSparseAttention.apply(q, k, v, block_mask, layout)
+        return (out, lse) if return_lse else out
     lists = index_lists(block_mask, layout)
     return block_sparse_attention_lists(q, k, v, lists, layout, return_lse)
 

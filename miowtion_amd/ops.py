@@ -262,6 +262,73 @@ def _(q, k, v, part_cnt, part_idx, full_cnt, full_idx, valid_count, return_lse):
     return [out]
 
 
+def _check_lists(name: str, cnt: torch.Tensor, idx: torch.Tensor, heads: int, rows: int,
+                 cols: int) -> None:
+    if (idx.dtype != torch.int32 or idx.dim() != 4 or tuple(idx.shape[:3]) != (1, heads, rows)
+            or idx.shape[3] < cols or not idx.is_contiguous()):
+        raise ValueError(f'{name} index must be contiguous int32 [1, {heads}, {rows}, >= {cols}]')
+    if cnt.dtype != torch.int32 or cnt.numel() != heads * rows or not cnt.is_contiguous():
+        raise ValueError(f'{name} count must be contiguous int32 [1, {heads}, {rows}]')
+
+
+@torch.library.custom_op('veda::block_sparse_bwd', mutates_args=())
+def block_sparse_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                     dout: torch.Tensor, lse: torch.Tensor, dlse: torch.Tensor | None,
+                     part_cnt: torch.Tensor, part_idx: torch.Tensor, full_cnt: torch.Tensor,
+                     full_idx: torch.Tensor, part_cnt_t: torch.Tensor, part_idx_t: torch.Tensor,
+                     full_cnt_t: torch.Tensor, full_idx_t: torch.Tensor,
+                     valid_count: torch.Tensor) -> list[torch.Tensor]:
+    """-> [dq, dk, dv] of block_sparse_fwd (fa4_sm8x/interface.py:2099
+    _flash_attn_bwd with the Q-direction lists). lse: the forward's [H', R*128]
+    fp32 LSE; dlse: its gradient or None; *_t: index_lists(transpose=True)."""
+    _require_gpu(q, k, v, out, dout, lse, dlse, part_cnt, part_idx, full_cnt, full_idx,
+                 part_cnt_t, part_idx_t, full_cnt_t, full_idx_t, valid_count)
+    for name, t in (('q', q), ('k', k), ('v', v), ('out', out), ('dout', dout)):
+        _check_rows(name, t)
+    if q.shape[-1] != 128:
+        raise ValueError('block_sparse_bwd supports head_dim 128')
+    rq, heads, d = q.shape
+    if (rq % TILE or k.shape[0] % TILE or k.shape != v.shape or k.shape[1:] != q.shape[1:]
+            or out.shape != q.shape or dout.shape != q.shape):
+        raise ValueError(f'bad shapes q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)} '
+                         f'out {tuple(out.shape)} dout {tuple(dout.shape)}')
+    r_tiles, n_k = rq // TILE, k.shape[0] // TILE
+    for name, t in (('lse', lse), ('dlse', dlse)):
+        if t is not None and (t.dtype != torch.float32 or tuple(t.shape) != (heads, rq)):
+            raise ValueError(f'{name} must be fp32 [{heads}, {rq}]')
+    _check_lists('part', part_cnt, part_idx, heads, r_tiles, n_k)
+    _check_lists('full', full_cnt, full_idx, heads, r_tiles, n_k)
+    _check_lists('transposed part', part_cnt_t, part_idx_t, heads, n_k, r_tiles)
+    _check_lists('transposed full', full_cnt_t, full_idx_t, heads, n_k, r_tiles)
+    if part_idx.shape[3] != full_idx.shape[3] or part_idx_t.shape[3] != full_idx_t.shape[3]:
+        raise ValueError('the part and full lists of one direction must have equal rows')
+    if valid_count.numel() < n_k or valid_count.dtype != torch.int32:
+        raise ValueError('valid_count must be int32 [n_k_tiles]')
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    work = torch.empty(max(heads * r_tiles * 512, 4), dtype=torch.float32, device=q.device)
+    _native.call('veda_block_sparse_bwd', q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(),
+                 k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+                 out.data_ptr(), out.stride(0), out.stride(1), dout.data_ptr(), dout.stride(0),
+                 dout.stride(1), lse.data_ptr(), lse.stride(0), lse.stride(1), _p(dlse),
+                 0 if dlse is None else dlse.stride(0), 0 if dlse is None else dlse.stride(1),
+                 heads, d, r_tiles, n_k, full_cnt.data_ptr(), full_idx.data_ptr(),
+                 part_cnt.data_ptr(), part_idx.data_ptr(), part_idx.shape[3],
+                 full_cnt_t.data_ptr(), full_idx_t.data_ptr(), part_cnt_t.data_ptr(),
+                 part_idx_t.data_ptr(), part_idx_t.shape[3], valid_count.data_ptr(),
+                 1.0 / math.sqrt(d), dq.data_ptr(), dq.stride(0), dq.stride(1), dk.data_ptr(),
+                 dk.stride(0), dk.stride(1), dv.data_ptr(), dv.stride(0), dv.stride(1),
+                 work.data_ptr(), work.numel() * 4, _stream(q))
+    return [dq, dk, dv]
+
+
+@block_sparse_bwd.register_fake
+def _(q, k, v, out, dout, lse, dlse, part_cnt, part_idx, full_cnt, full_idx, part_cnt_t,
+      part_idx_t, full_cnt_t, full_idx_t, valid_count):
+    return [torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)]
+
+
 @torch.library.custom_op('veda::dense_fwd', mutates_args=())
 def dense_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, used: int,
               return_lse: bool) -> list[torch.Tensor]:

@@ -7,6 +7,9 @@ Restates:
                             -> `miowtion/h3/attention.py:18-25,80-102`
   * teacher_heat_reference  -> `miowtion/veda/heatmap.py:36-99`
   * zero_order_compensation -> `miowtion/veda/attention.py:591-689`
+  * block_sparse_attention_grads -> autograd through
+      `miowtion/kernels/reference.py:23-56`, the expected gradients of
+      `tests/gpu/test_kernels_gpu.py:200-250`
 
 The reference materialises [H', N, N]; this restatement does the same math
 per head and per chunk of query rows so that C2-sized heads fit in memory.
@@ -23,29 +26,58 @@ from oracle.tiling import TILE, Layout
 
 
 def block_sparse_attention(q, k, v, block_mask, valid_count, return_lse=False,
-                           q_chunk: int = 1024):
+                           q_chunk: int = 1024, compute_dtype=torch.float32):
     """q [R*128, H', D], k/v [N, H', D], block_mask [H', R, n] -> out in
-    q.dtype (and lse [H', R*128] fp32, -inf for rows with no key)."""
+    q.dtype (and lse [H', R*128] in compute_dtype, -inf for rows with no
+    key). The reference computes in fp32; float64 serves the
+    finite-difference checks of the gradients."""
     Rq, H, D = q.shape
     N = k.shape[0]
     scale = 1.0 / math.sqrt(D)
     key_valid = (torch.arange(TILE)[None, :] < valid_count[:, None]).reshape(-1)[:N]
-    out = torch.empty(Rq, H, D, dtype=torch.float32)
-    lse = torch.empty(H, Rq, dtype=torch.float32)
-    kf, vf = k.float(), v.float()
+    out = torch.empty(Rq, H, D, dtype=compute_dtype)
+    lse = torch.empty(H, Rq, dtype=compute_dtype)
+    kf, vf = k.to(compute_dtype), v.to(compute_dtype)
     for h in range(H):
         bm = block_mask[h]
         for q0 in range(0, Rq, q_chunk):
             q1 = min(q0 + q_chunk, Rq)
             rows = torch.arange(q0, q1) // TILE
             tok = bm[rows].repeat_interleave(TILE, 1)[:, :N] & key_valid[None, :]
-            s = (q[q0:q1, h].float() @ kf[:, h].T) * scale
+            s = (q[q0:q1, h].to(compute_dtype) @ kf[:, h].T) * scale
             s = s.masked_fill(~tok, float('-inf'))
             p = torch.softmax(s, -1).nan_to_num(0.0)
             out[q0:q1, h] = p @ vf[:, h]
             lse[h, q0:q1] = torch.logsumexp(s, -1)
     o = out.to(q.dtype)
     return (o, lse) if return_lse else o
+
+
+def block_sparse_attention_grads(q, k, v, block_mask, valid_count, dout, dlse=None,
+                                 dtype=torch.float32):
+    """dq, dk, dv of block_sparse_attention for the loss
+    sum(out * dout) (+ sum(lse * dlse) over rows that have a key), by
+    autograd through the same masked softmax, one head at a time, computed in
+    `dtype` (float64 for the finite-difference checks). Returns them in
+    `dtype`; a row with no key gets no gradient."""
+    Rq, H, D = q.shape
+    N = k.shape[0]
+    scale = 1.0 / math.sqrt(D)
+    key_valid = (torch.arange(TILE)[None, :] < valid_count[:, None]).reshape(-1)[:N]
+    grads = [torch.zeros(t.shape, dtype=dtype) for t in (q, k, v)]
+    for h in range(H):
+        qh, kh, vh = (t[:, h].to(dtype).requires_grad_(True) for t in (q, k, v))
+        tok = (block_mask[h].repeat_interleave(TILE, 0)[:Rq].repeat_interleave(TILE, 1)[:, :N]
+               & key_valid[None, :])
+        s = ((qh @ kh.T) * scale).masked_fill(~tok, float('-inf'))
+        p = torch.softmax(s, -1).nan_to_num(0.0)
+        loss = ((p @ vh) * dout[:, h].to(dtype)).sum()
+        if dlse is not None:
+            rows = tok.any(-1)
+            loss = loss + (torch.logsumexp(s[rows], -1) * dlse[h, rows].to(dtype)).sum()
+        gq, gk, gv = torch.autograd.grad(loss, (qh, kh, vh))
+        grads[0][:, h], grads[1][:, h], grads[2][:, h] = gq, gk, gv
+    return tuple(grads)
 
 
 def dense_attention(q, k, v, used: int, return_lse=False, q_chunk: int = 1024):

@@ -129,9 +129,14 @@ def pack_lists(member: torch.Tensor):
             torch.gather(idx, -1, order)[None].to(torch.int32).contiguous())
 
 
-def index_lists(block_mask: torch.Tensor, lay: Layout):
-    """fa4.py:275-296 -> (part_cnt, part_idx, full_cnt, full_idx)."""
+def index_lists(block_mask: torch.Tensor, lay: Layout, transpose: bool = False):
+    """fa4.py:275-296 -> (part_cnt, part_idx, full_cnt, full_idx); transpose:
+    the Q-direction lists (rows = key tiles, split by the row's fullness)."""
     m = block_mask & lay.kv_ok
-    fc, fi = pack_lists(m & lay.full_tile)
-    pc, pi = pack_lists(m & ~lay.full_tile)
+    full = lay.full_tile
+    if transpose:
+        m = m.transpose(1, 2)
+        full = full[:, None]
+    fc, fi = pack_lists(m & full)
+    pc, pi = pack_lists(m & ~full)
     return pc, pi, fc, fi

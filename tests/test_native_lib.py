@@ -36,7 +36,7 @@ def test_library_built_and_exports_every_declared_symbol():
             continue
         assert len(_native.SIGNATURES[name]) == n, name
     assert set(_native.SIGNATURES) <= set(declared)
-    assert lib.veda_abi_version() == 3
+    assert lib.veda_abi_version() == 4
 
 
 def test_host_side_argument_checks():
@@ -66,6 +66,14 @@ def test_host_side_argument_checks():
     with pytest.raises(ValueError, match='out and v'):
         _native.call('veda_dense_heat_fwd', 16, 0, 0, 1, 16, 0, 0, 16, 0, 0, 1, 128, None,
                      1, 1, None, 1.0, 0, None, 0, 0, 16, 0, 0, 16, None)
+    with pytest.raises(ValueError, match='head_dim'):
+        _native.call('veda_block_sparse_bwd', *([None, 0, 0] * 7), 1, 64, 1, 1, None, None,
+                     None, None, 1, None, None, None, None, 1, None, 1.0, *([None, 0, 0] * 3),
+                     None, 0, None)
+    with pytest.raises(ValueError, match='workspace'):
+        _native.call('veda_block_sparse_bwd', *([16, 0, 0] * 5), 16, 0, 0, None, 0, 0, 1, 128,
+                     1, 1, None, None, None, None, 1, None, None, None, None, 1, None, 1.0,
+                     *([16, 0, 0] * 3), 16, 1024, None)
     with pytest.raises(ValueError, match='reduce'):
         _native.call('veda_heat_combine', None, None, 0, 0, None, None, 1, 1, 1, 5, None, None)
     assert isinstance(lib.veda_last_error(), bytes)
