@@ -195,6 +195,20 @@ def suite(reps: int = 5) -> dict:
     ms = _median_ms(lambda: kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'],
                                                                  c['lists'], lay), reps)
     res['sparse_fwd_c2'] = _mfma(ms, 4.0 * 128 * 128 * D * kept)
+    # block-sparse backward (stage-2 training) given the forward's out and LSE:
+    # 5 products of 2 * 128 * 128 * D per kept block (S, dP, dV, dK, dQ; the
+    # dQ kernel's recomputation of S and dP is not counted)
+    from miowtion_amd import ops
+    lists_t = kernels.index_lists(c['mask'], lay, transpose=True)
+    o_f, lse_f = kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'], c['lists'], lay,
+                                                      return_lse=True)
+    dout = torch.randn(o_f.shape, generator=torch.Generator(device='cuda').manual_seed(3),
+                       device='cuda').to(torch.bfloat16)
+    ms_b = _median_ms(lambda: ops.block_sparse_bwd(c['qt'], c['kt'], c['vt'], o_f, dout, lse_f, None,
+                                                   *c['lists'], *lists_t, lay.valid_count), reps)
+    res['sparse_bwd_c2'] = _mfma(ms_b, 10.0 * 128 * 128 * D * kept)
+    res['sparse_bwd_c2']['vs_sparse_fwd'] = round(ms_b / ms, 3)
+    del lists_t, o_f, lse_f, dout
     # zero-order compensation of the dropped tiles (summaries + the virtual-key
     # pass; the reference's Triton form costs 1.14x its sparse kernel)
     o_kept, lse_kept = kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'], c['lists'],
@@ -275,6 +289,39 @@ def suite(reps: int = 5) -> dict:
     return res
 
 
+def _backward(c: dict, kept: int, steps: int, warmup: int) -> int:
+    """The block-sparse backward at C2 given the forward's out and LSE (one
+    veda_block_sparse_bwd call: stats, dQ and dK/dV kernels); TFLOP/s on 5
+    products of 2 * 128^3 per kept block."""
+    from miowtion_amd import kernels, ops
+    lay = c['lay']
+    lists_t = kernels.index_lists(c['mask'], lay, transpose=True)
+    o, lse = kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'], c['lists'], lay,
+                                                  return_lse=True)
+    dout = torch.randn(o.shape, generator=torch.Generator(device='cuda').manual_seed(3),
+                       device='cuda').to(torch.bfloat16)
+
+    def step():
+        return ops.block_sparse_bwd(c['qt'], c['kt'], c['vt'], o, dout, lse, None, *c['lists'],
+                                    *lists_t, lay.valid_count)
+
+    _log(f'bench: backward, warmup {warmup}')
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    _log(f'bench: backward, timing {steps} steps')
+    ms = sorted(_events_ms(step, max(5, steps)))
+    med, avg = ms[len(ms) // 2], sum(ms) / len(ms)
+    flop = 10.0 * 128 * 128 * D * kept
+    print(json.dumps({'metric': 'block-sparse attention backward TFLOP/s @C2 (5 products per '
+                                'kept block)',
+                      'value': round(flop / (med * 1e-3) / 1e12, 2), 'ms_per_step': round(med, 4),
+                      'avg_launch_ms': round(avg, 4), 'flop_per_launch': flop,
+                      'frac_of_bf16_peak': round(flop / (med * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                      'kept_blocks': kept}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -285,6 +332,8 @@ def main() -> int:
     ap.add_argument('--cpu-budget', type=float, default=20.0)
     ap.add_argument('--only-kernel', action='store_true',
                     help='time the sparse forward only (for rocprofv3 runs)')
+    ap.add_argument('--backward', action='store_true',
+                    help='time the block-sparse backward at C2 only (for rocprofv3 runs)')
     ap.add_argument('--suite', action='store_true',
                     help='time every kernel of the path at its BASELINE config against its '
                          'roofline and print that JSON instead of the headline line')
@@ -315,6 +364,8 @@ def main() -> int:
     lay = c['lay']
     kept = int(c['mask'].sum())
     assert kept == 20340 * HEADS, kept
+    if args.backward:
+        return _backward(c, kept, args.steps, args.warmup)
     flop = 4.0 * 128 * 128 * D * kept
     # What the kernel executes: the valid keys of every kept block (padding
     # rows of partial key tiles are neither loaded nor multiplied); query
