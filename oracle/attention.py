@@ -9,7 +9,8 @@ Restates:
   * zero_order_compensation -> `miowtion/veda/attention.py:591-689`
   * block_sparse_attention_grads -> autograd through
       `miowtion/kernels/reference.py:23-56`, the expected gradients of
-      `tests/gpu/test_kernels_gpu.py:200-250`
+      `tests/gpu/test_kernels_gpu.py:200-250` (and a per-tile form of the
+      same autograd that scales with the kept blocks)
 
 The reference materialises [H', N, N]; this restatement does the same math
 per head and per chunk of query rows so that C2-sized heads fit in memory.
@@ -77,6 +78,42 @@ def block_sparse_attention_grads(q, k, v, block_mask, valid_count, dout, dlse=No
             loss = loss + (torch.logsumexp(s[rows], -1) * dlse[h, rows].to(dtype)).sum()
         gq, gk, gv = torch.autograd.grad(loss, (qh, kh, vh))
         grads[0][:, h], grads[1][:, h], grads[2][:, h] = gq, gk, gv
+    return tuple(grads)
+
+
+def block_sparse_attention_grads_by_tile(q, k, v, block_mask, valid_count, dout, dlse=None,
+                                         dtype=torch.float32):
+    """Same gradients as block_sparse_attention_grads, one (head, query tile)
+    at a time over only its kept key tiles' valid keys: every row's softmax
+    is over exactly those keys, so the restriction is exact, and the key
+    gradients of the tiles are summed. Cost scales with the kept blocks, so
+    it runs at the BASELINE sizes; block_mask may hold a subset of query
+    tiles only if dout covers the same rows (then dk, dv are that subset's
+    share)."""
+    Rq, H, D = q.shape
+    scale = 1.0 / math.sqrt(D)
+    vc = valid_count.tolist()
+    grads = [torch.zeros(t.shape, dtype=dtype) for t in (q, k, v)]
+    for h in range(H):
+        kh_all, vh_all = k[:, h].to(dtype), v[:, h].to(dtype)
+        for i in range(Rq // TILE):
+            cols = torch.nonzero(block_mask[h, i]).flatten().tolist()
+            rows = [torch.arange(j * TILE, j * TILE + vc[j]) for j in cols if vc[j] > 0]
+            if not rows:
+                continue
+            idx = torch.cat(rows)
+            qi = q[i * TILE:(i + 1) * TILE, h].to(dtype).requires_grad_(True)
+            ki = kh_all[idx].requires_grad_(True)
+            vi = vh_all[idx].requires_grad_(True)
+            s = (qi @ ki.T) * scale
+            loss = ((torch.softmax(s, -1) @ vi) * dout[i * TILE:(i + 1) * TILE, h].to(dtype)).sum()
+            if dlse is not None:
+                loss = loss + (torch.logsumexp(s, -1)
+                               * dlse[h, i * TILE:(i + 1) * TILE].to(dtype)).sum()
+            gq, gk, gv = torch.autograd.grad(loss, (qi, ki, vi))
+            grads[0][i * TILE:(i + 1) * TILE, h] = gq
+            grads[1][:, h].index_add_(0, idx, gk)
+            grads[2][:, h].index_add_(0, idx, gv)
     return tuple(grads)
 
 

@@ -148,3 +148,28 @@ def test_subset_of_query_tiles_refused():
     with torch.no_grad():
         out = kernels.block_sparse_attention(q, kt, vt, mask[:, :2], lay)
     assert out.shape == q.shape
+
+
+def test_config2_two_heads():
+    """BASELINE config 2 geometry (592 tiles, keep 0.1), 2 heads: every
+    gradient row against the oracle's per-tile autograd, which is exact and
+    scales with the kept blocks."""
+    spans, used, seq_len, shape = helpers.CONFIGS['C2']
+    lay = helpers.product_layout(spans, used, seq_len, shape, device='cuda')
+    olay = helpers.oracle_layout(spans, used, seq_len, shape)
+    H = 2
+    print(f'C2 backward: {lay.n_tiles} tiles, {H} heads', flush=True)
+    g = torch.Generator(device='cuda').manual_seed(5)
+    q, k, v = (torch.randn(seq_len, H, 128, generator=g, device='cuda').to(torch.bfloat16)
+               for _ in range(3))
+    qt, kt, vt = (kernels.gather_tiles(t, lay, None) for t in (q, k, v))
+    scores = torch.rand(H, lay.n_tiles, lay.n_tiles, generator=g, device='cuda')
+    sel = pm.select_video_blocks(scores, lay, pm.column_blocks(lay, pm.Budget(ratio=0.1)))
+    mask = pm.dense_block_mask(sel, lay)
+    grad_out = torch.randn(qt.shape, generator=g, device='cuda').to(torch.bfloat16)
+    got = _gpu_grads(qt, kt, vt, mask, lay, grad_out)
+    want = oa.block_sparse_attention_grads_by_tile(qt.cpu(), kt.cpu(), vt.cpu(),
+                                                   (mask & lay.kv_ok[None, None, :]).cpu(),
+                                                   olay.valid_count, grad_out.cpu().float())
+    for name, a, w in zip('qkv', got, want):
+        _bar(a, w, name)

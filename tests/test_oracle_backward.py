@@ -11,7 +11,9 @@ use autograd or restate the gradient formulas:
   * block structure: a key tile no query tile keeps, padding keys and a
     query tile that keeps nothing get exactly zero gradient;
   * the transposed index lists (fa4.py:288-296) list, per key tile, exactly
-    the query tiles that keep it.
+    the query tiles that keep it;
+  * the per-tile form (used at the BASELINE sizes) equals the masked-dense
+    form.
 """
 
 import torch
@@ -117,3 +119,17 @@ def test_transposed_lists():
                                         dtype=torch.float64)
     for x, y in zip(a, b):
         torch.testing.assert_close(2 * x, y, rtol=1e-12, atol=1e-12)
+
+
+def test_by_tile_form_equals_masked_dense_form():
+    lay, q, k, v, mask, g = _case(4, heads=3)
+    m = mask.clone()
+    m[1, 0, :] = False  # a query tile with no key
+    dout = torch.randn(q.shape, generator=g, dtype=torch.float64)
+    dlse = torch.randn(q.shape[1], q.shape[0], generator=g, dtype=torch.float64)
+    a = oa.block_sparse_attention_grads(q, k, v, m & lay.kv_ok, lay.valid_count, dout, dlse,
+                                        dtype=torch.float64)
+    b = oa.block_sparse_attention_grads_by_tile(q, k, v, m, lay.valid_count, dout, dlse,
+                                                dtype=torch.float64)
+    for x, y in zip(a, b):
+        torch.testing.assert_close(x, y, rtol=1e-10, atol=1e-10)
