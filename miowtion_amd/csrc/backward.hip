@@ -46,7 +46,7 @@ constexpr int kMaxTiles = 2048;                  // tiles per list row (FA4's ca
 constexpr int kRecFloats = 256;                  // stats record: 64 lse2, 64 D, 128 zero
 constexpr int kRecBytes = kRecFloats * 4;
 constexpr int kDqThreads = 512;
-constexpr int kDkvThreads = 256;
+constexpr int kDkvThreads = 512;
 constexpr int kSlot = 2 * kHalfBytes;            // K + V (dq) or Q + dO (dkv) of a step
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -380,24 +380,34 @@ __global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV. Workgroup = (head, key tile), 4 waves: wave w owns keys
-// 32 w .. + 31 of the tile (one per lane, as B = K^T and V^T fragments in
-// registers) and their dK^T, dV^T accumulators. Per 64-row query step and
-// 32-row half of it: S = Q K^T and dP = dO V^T (8 MFMAs each, A = Q / dO
-// rows from LDS), P and dS, then dV^T += dO^T P and dK^T += Q^T dS (8 MFMAs
-// each, A = transposed dO / Q reads). The step's lse2 and D come with it.
+// dK, dV. Workgroup = (head, key tile), 8 waves, two per key group: waves
+// g and g + 4 (which share a SIMD) own keys 32 g .. + 31 of the tile (one
+// per lane). Per 64-row query step, in two phases split by a barrier:
+//   wave g     (K^T in registers): S = Q K^T for both 32-row halves
+//              (16 MFMAs, A = Q rows from LDS), P = exp2(S c - lse2), P to
+//              LDS; then dV^T += dO^T P (16 MFMAs, transposed dO reads);
+//   wave g + 4 (V^T in registers): dP = dO V^T (16 MFMAs); then P from LDS,
+//              dS = P (dP - D), dK^T += Q^T dS (16 MFMAs, transposed Q reads).
+// Each wave holds one 128 x 32 fp32 accumulator, so two waves fit a SIMD and
+// one's exponentials overlap the other's MFMAs. P crosses in fp32, so dS
+// uses the same P as the single-wave form. The step's lse2 and D come with it.
 
-__global__ void __launch_bounds__(kDkvThreads, 1) dkv_kernel(BwdParams p) {
+constexpr int kXBytes = 4 * 2 * 64 * 16 * 4;  // P exchange: 4 key groups x 2 halves
+
+__global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[2][kSlot + kRecBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t xbuf[kXBytes];
   __shared__ uint16_t steps[2 * kMaxTiles];
   __shared__ int32_t step_total;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 31, hi = lane >> 5;
+  const int kg = wave & 3;
+  const bool pwave = wave < 4;  // S, P, dV; else dP, dS, dK
   const int64_t item = blockIdx.x;
   const int64_t head = item / p.n_k_tiles, j = item % p.n_k_tiles;
   const int vc = __builtin_amdgcn_readfirstlane(clamp_vc(p.valid_count[j]));
-  const int64_t krow = j * kTile + 32 * wave + li;
+  const int64_t krow = j * kTile + 32 * kg + li;
   const int nq = (int)p.n_q_tiles;
 
   if (wave == 0) {
@@ -410,35 +420,32 @@ __global__ void __launch_bounds__(kDkvThreads, 1) dkv_kernel(BwdParams p) {
     if (lane == 0) step_total = n;
   }
 
-  bf16x8 kf[8], vf[8];
+  // B operand rows: K (P-wave) or V (dS-wave) of this lane's key
+  const uint16_t* brow = pwave ? p.k + krow * p.ks + head * p.kh : p.v + krow * p.vs + head * p.vh;
+  bf16x8 bf[8];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    kf[s] = as_bf16x8(ld16(p.k + krow * p.ks + head * p.kh + 16 * s + 8 * hi));
-    vf[s] = as_bf16x8(ld16(p.v + krow * p.vs + head * p.vh + 16 * s + 8 * hi));
-  }
-  f32x16 dk[4], dv[4];
+  for (int s = 0; s < 8; ++s) bf[s] = as_bf16x8(ld16(brow + 16 * s + 8 * hi));
+  f32x16 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      dk[dt][e] = 0.f;
-      dv[dt][e] = 0.f;
-    }
+    for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
   __syncthreads();
   const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
 
   const uint16_t* qbase = p.q + head * p.qh;
   const uint16_t* dbase = p.dout + head * p.doh;
-  uint32_t qoff[4], doff[4];
+  uint32_t qoff[2], doff[2];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    qoff[u] = seg_offset(4 * wave + u, lane, p.qs);
-    doff[u] = seg_offset(4 * wave + u, lane, p.dos);
+  for (int u = 0; u < 2; ++u) {
+    qoff[u] = seg_offset(2 * wave + u, lane, p.qs);
+    doff[u] = seg_offset(2 * wave + u, lane, p.dos);
   }
   const Frag f = frag_offsets(lane);
   const float c = p.scale_log2;
-  const bool key_ok = 32 * wave + li < vc;
-  const bool wave_live = 32 * wave < vc;
+  const bool key_ok = 32 * kg + li < vc;
+  const bool live = 32 * kg < vc;
+  lds_u8* xb = (lds_u8*)xbuf + kg * 2 * 4096 + lane * 16;  // + qt * 4096 + e4 * 1024
 
   auto load_step = [&](int u, lds_u8* slot) {
     const int t = __builtin_amdgcn_readfirstlane(steps[u]);
@@ -446,77 +453,105 @@ __global__ void __launch_bounds__(kDkvThreads, 1) dkv_kernel(BwdParams p) {
     const char* qb = reinterpret_cast<const char*>(qbase + row0 * p.qs);
     const char* db = reinterpret_cast<const char*>(dbase + row0 * p.dos);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      dma16(qb, qoff[s], slot + (4 * wave + s) * 1024);
-      dma16(db, doff[s], slot + kHalfBytes + (4 * wave + s) * 1024);
+    for (int s = 0; s < 2; ++s) {
+      dma16(qb, qoff[s], slot + (2 * wave + s) * 1024);
+      dma16(db, doff[s], slot + kHalfBytes + (2 * wave + s) * 1024);
     }
     if (wave == 0) {
       const float* rec = p.stats + (head * 2 * p.n_q_tiles + t) * kRecFloats;
       dma16(reinterpret_cast<const char*>(rec), (uint32_t)(lane * 16), slot + kSlot);
     }
   };
-  auto compute = [&](const lds_u8* slot) {
-    const lds_u8* qs = slot;
-    const lds_u8* ds_ = slot + kHalfBytes;
+
+  // Phase 1: S and P (P-wave) or dP (dS-wave) of both 32-row halves.
+  f32x16 sd[2];
+  u32x4 pk[2][2];
+  auto phase1 = [&](const lds_u8* slot) {
+    const lds_u8* a = pwave ? slot : slot + kHalfBytes;  // Q or dO rows
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sd[qt][e] = 0.f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        sd[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(a + qt * 8192 + f.row[s])),
+                                                         bf[s], sd[qt], 0, 0, 0);
+    }
+    if (!pwave) return;
     const lds_u8* sr = slot + kSlot;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      const lds_u8* qq = qs + qt * 8192;
-      const lds_u8* dd = ds_ + qt * 8192;
-      f32x16 sv, dp;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        sv[e] = 0.f;
-        dp[e] = 0.f;
-      }
-#pragma unroll
-      for (int s = 0; s < 8; ++s)
-        sv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(qq + f.row[s])), kf[s], sv, 0, 0, 0);
-#pragma unroll
-      for (int s = 0; s < 8; ++s)
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(dd + f.row[s])), vf[s], dp, 0, 0, 0);
-      // rows 32 qt + 8 g + 4 hi + {0..3} of the step
-      float pr[16], dsv[16];
+      float pr[16];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int r0 = 32 * qt + 8 * g + 4 * hi;
-        const f32x4 l4 = *reinterpret_cast<const lds_f32x4*>(sr + 4 * r0);
-        const f32x4 d4 = *reinterpret_cast<const lds_f32x4*>(sr + 256 + 4 * r0);
+        const f32x4 l4 = *reinterpret_cast<const lds_f32x4*>(sr + 4 * (32 * qt + 8 * g + 4 * hi));
+        f32x4 p4;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const int e = 4 * g + m;
-          float x = __builtin_amdgcn_exp2f(fmaf(sv[e], c, -l4[m]));
-          x = key_ok ? x : 0.f;
-          pr[e] = x;
-          dsv[e] = x * (dp[e] - d4[m]);
+          const float x = __builtin_amdgcn_exp2f(fmaf(sd[qt][4 * g + m], c, -l4[m]));
+          p4[m] = key_ok ? x : 0.f;
+          pr[4 * g + m] = p4[m];
+        }
+        *reinterpret_cast<lds_f32x4*>(xb + qt * 4096 + g * 1024) = p4;
+      }
+      pack_b(pr, pk[qt]);
+    }
+  };
+  // Phase 2: dV^T += dO^T P (P-wave) or dS and dK^T += Q^T dS (dS-wave).
+  auto phase2 = [&](const lds_u8* slot) {
+    if (pwave) {
+      const lds_u8* dd = slot + kHalfBytes;
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt)
+            acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                tr_frag(dd + qt * 8192, f, dt, kk), as_bf16x8(pk[qt][kk]), acc[dt], 0, 0, 0);
+      return;
+    }
+    const lds_u8* sr = slot + kSlot;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float dsv[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 d4 = *reinterpret_cast<const lds_f32x4*>(sr + 256 + 4 * (32 * qt + 8 * g + 4 * hi));
+        const f32x4 p4 = *reinterpret_cast<const lds_f32x4*>(xb + qt * 4096 + g * 1024);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const float x = p4[m] * (sd[qt][4 * g + m] - d4[m]);
+          dsv[4 * g + m] = key_ok ? x : 0.f;
         }
       }
-      u32x4 pk[2], sk[2];
-      pack_b(pr, pk);
+      u32x4 sk[2];
       pack_b(dsv, sk);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
-          dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag(dd, f, dt, kk), as_bf16x8(pk[kk]),
-                                                           dv[dt], 0, 0, 0);
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-          dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag(qq, f, dt, kk), as_bf16x8(sk[kk]),
-                                                           dk[dt], 0, 0, 0);
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag(slot + qt * 8192, f, dt, kk),
+                                                            as_bf16x8(sk[kk]), acc[dt], 0, 0, 0);
     }
   };
 
   lds_u8* s0 = (lds_u8*)ring[0];
   lds_u8* s1 = (lds_u8*)ring[1];
+  // Step u: loads of step u landed and the other slot and the P buffer are
+  // free (barrier 1); phase 1; P visible to the partner wave (LDS writes
+  // done, barrier 2); phase 2. Both barriers are reached by every wave.
   auto run = [&](int u, lds_u8* cur, lds_u8* nxt) {
     VEDA_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");  // no LDS read of step u above the barrier
+    asm volatile("" ::: "memory");
     if (u + 1 < n_steps) load_step(u + 1, nxt);
-    if (wave_live) compute(cur);
+    if (live) phase1(cur);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's P stores are in LDS
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (live) phase2(cur);
   };
   if (n_steps > 0) load_step(0, s0);
   for (int u = 0; u < n_steps; u += 2) {
@@ -524,18 +559,13 @@ __global__ void __launch_bounds__(kDkvThreads, 1) dkv_kernel(BwdParams p) {
     if (u + 1 >= n_steps) break;
     run(u + 1, s1, s0);
   }
-  VEDA_WAIT_VM(0);
 
-  uint16_t* krow_p = p.dk + krow * p.dks + head * p.dkh;
-  uint16_t* vrow_p = p.dv + krow * p.dvs + head * p.dvh;
+  uint16_t* orow = pwave ? p.dv + krow * p.dvs + head * p.dvh : p.dk + krow * p.dks + head * p.dkh;
+  const float mul = pwave ? 1.f : p.scale;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = 32 * dt + 8 * g + 4 * hi;
-      store4(krow_p, d, dk[dt], 4 * g, p.scale);
-      store4(vrow_p, d, dv[dt], 4 * g, 1.f);
-    }
+    for (int g = 0; g < 4; ++g) store4(orow, 32 * dt + 8 * g + 4 * hi, acc[dt], 4 * g, mul);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
