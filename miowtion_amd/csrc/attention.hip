@@ -1,7 +1,10 @@
-// Block-sparse flash-attention forward for gfx950 (head_dim 128, bf16 in,
-// fp32 accumulate), and the dense forward built from the same kernel.
+// Flash-attention forwards for gfx950 (head_dim 128, bf16 in, fp32
+// accumulate). Two kernels share the step, fragment and load code below:
+//   hfwd_kernel  the dense forward and the teacher's all-tiles pass;
+//   sfwd_kernel  the block-sparse forward and the zero-order compensation
+//                (two 4-wave workgroups per CU, described at its section).
 //
-// Workgroup = one (head, 128-row query tile), 8 waves, 1 workgroup per CU:
+// hfwd_kernel: workgroup = one (head, 128-row query tile), 8 waves, 1 per CU:
 //   wave w: query group qg = w & 3 (32 query rows), key half kh = w >> 2;
 //   waves w and w + 4 share a SIMD, so one wave's softmax can overlap the
 //   other's MFMAs. The two key halves keep separate online-softmax states
@@ -81,7 +84,7 @@ struct FwdParams {
 // Key walks: the block lists (sparse forward), every row of a packed
 // sequence (dense forward), or every key tile of a tile layout in order,
 // its padding rows masked (the teacher's dense pass in tile order).
-enum Walk { kLists = 0, kDense = 1, kAllTiles = 2, kVirtual = 3 };
+enum Walk { kLists = 0, kDense = 1, kAllTiles = 2 };
 // Block statistic collected for the teacher heat: none, log-sum-exp, max.
 enum Heat { kNoHeat = 0, kHeatSum = 1, kHeatMax = 2 };
 constexpr int32_t kTileEnd = 1 << 30;  // step-list flag: last step of its key tile
@@ -277,63 +280,10 @@ __device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float 
 }
 
 
-// Zero-order compensation step: this wave's 32 virtual keys of the step
-// (tile summaries: key = mean K of a key tile, value = sum V) against its
-// 32 query rows, with the fixed reference ref2 = lse_kept log2 e of the
-// row instead of an online max. wt[j] is the real row count of key tile j
-// if the mask dropped it, else 0: p = exp2(s c - ref2) where wt > 0, the
-// denominator gains p wt, and O^T += V^T P^T as in the attention step.
-__device__ __forceinline__ void vstep(const lds_u8* slot, const HFrag& f, float c,
-                                      const float* wt, int key0, int hi, float ref2,
-                                      WaveState& w) {
-  u32x4 kf[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k)
-    kf[k] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(slot + f.k[k]);
-  f32x16 s;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) s[e] = 0.f;
-#pragma unroll
-  for (int k = 0; k < 8; ++k)
-    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[k]), w.qf[k], s, 0, 0, 0);
-  // register e holds key key0 + 8 (e / 4) + 4 hi + e % 4
-  float ps[16], den = 0.f;
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const f32x4 ww = *reinterpret_cast<const f32x4*>(wt + key0 + 8 * g + 4 * hi);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const float x = ww[m] > 0.f ? __builtin_amdgcn_exp2f(fmaf(s[4 * g + m], c, -ref2)) : 0.f;
-      ps[4 * g + m] = x;
-      den = fmaf(x, ww[m], den);
-    }
-  }
-  w.l_run += den;
-  u32x4 pk[2];
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-    for (int m = 0; m < 4; ++m) pk[kk][m] = pack_bf16x2(ps[8 * kk + 2 * m], ps[8 * kk + 2 * m + 1]);
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    const lds_u8* vs = slot + kk * 16 * 256;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + f.v[dt]));
-      const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + 8 * 256 + f.v[dt]));
-      const bf16x8 a =
-          __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
-      w.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pk[kk]), w.o[dt], 0, 0, 0);
-    }
-  }
-}
-
-
 template <int WALK, int HEAT, bool PV>
 __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   constexpr bool DENSE = WALK == kDense;
   constexpr bool TILES = WALK == kAllTiles;
-  constexpr bool VIRT = WALK == kVirtual;
   // Without PV a slot holds K only, and the all-tiles walk keeps its steps
   // as 16-bit (tile, half) entries plus a byte per tile of valid counts:
   // the statistics-only pass then needs 75 KB of LDS, so two workgroups
@@ -346,8 +296,6 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   __shared__ int32_t step_list[TILES ? 1 : 2 * kMaxBlocks];
   __shared__ uint16_t tile_steps[TILES ? 2 * kMaxBlocks : 1];  // (key tile << 1) | half
   __shared__ uint8_t tile_valid[TILES ? kMaxBlocks : 1];
-  // virtual-key walk: per key tile, its real row count if dropped, else 0
-  __shared__ __attribute__((aligned(16))) float vwt[VIRT ? kMaxBlocks + kHalf : 1];
   __shared__ int32_t step_total;
   __shared__ float lbuf[2][4][32];  // heat: kh = 1 hands its key-tile partials to kh = 0
   lds_u8* sl0 = (lds_u8*)slot0;
@@ -384,17 +332,6 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   if (DENSE) {
     const int64_t nsteps = (p.used + kHalf - 1) / kHalf;
     n_steps = (int)nsteps;
-  } else if (VIRT) {
-    // Virtual keys 0 .. n_k - 1 in steps of 64; the table is padded with
-    // zero weights to whole steps.
-    const int nk = (int)p.n_k_tiles;
-    n_steps = (nk + kHalf - 1) / kHalf;
-    const uint8_t* keep_row = p.keep + (head * p.n_q_tiles + r) * p.n_k_tiles;
-    for (int j = tid; j < n_steps * kHalf; j += kThreads) {
-      float wj = 0.f;
-      if (j < nk && keep_row[j] == 0) wj = (float)min(max(p.valid_count[j], 0), kTile);
-      vwt[j] = wj;
-    }
   } else if (TILES) {
     // Every key tile in order, its steps consecutive: the first half, then
     // the second half when more than 64 keys are valid; the tile's last step
@@ -476,7 +413,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   w.mu = 0.f;
   w.blk = HEAT == kHeatMax ? -INFINITY : 0.f;
   __syncthreads();  // step list, step count and zeroed ring ready
-  if (!DENSE && !VIRT) n_steps = __builtin_amdgcn_readfirstlane(step_total);
+  if (!DENSE) n_steps = __builtin_amdgcn_readfirstlane(step_total);
 
   // Step word of step u: (first key row << 7) | valid keys | kTileEnd.
   auto step_word = [&](int u) -> int32_t {
@@ -491,12 +428,12 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   };
   // (first key row, valid keys) of step u
   auto step_row = [&](int u) -> int64_t {
-    return (DENSE || VIRT) ? (int64_t)u * kHalf
+    return DENSE ? (int64_t)u * kHalf
                  : (int64_t)((step_word(u) >> 7) & 0x7FFFFF);
   };
   auto step_vch = [&](int u) -> int {
-    if (DENSE || VIRT) {
-      const int64_t rem = (VIRT ? p.n_k_tiles : p.used) - (int64_t)u * kHalf;
+    if (DENSE) {
+      const int64_t rem = p.used - (int64_t)u * kHalf;
       return rem < kHalf ? (int)rem : kHalf;
     }
     return step_word(u) & 127;
@@ -504,12 +441,6 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   const uint16_t* kbase = p.k + head * p.kh;
   const uint16_t* vbase = p.v + head * p.vh;
   const float c = p.scale_log2;
-  // compensation: the row's fixed reference (0 for a row that kept nothing)
-  float ref2 = 0.f;
-  if (VIRT) {
-    const float lk = p.lse_kept[head * p.lk_h + qrow * p.lk_s];
-    ref2 = (lk > -INFINITY && lk < INFINITY) ? lk * 1.4426950408889634f : 0.f;
-  }
   const HDma dma = hdma_offsets(p.ks, p.vs, wave, lane);
   const HFrag frag = hfrag_offsets(kh, lane);
 
@@ -517,7 +448,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
     const int vch = step_vch(u);
     // a step with no valid key (an empty or out-of-range tile) loads the
     // tile's first rows, which exist; its keys are all masked
-    if ((DENSE || VIRT) && vch < kHalf)
+    if (DENSE && vch < kHalf)
       issue_step<true, PV>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
     else
       issue_step<false, PV>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
@@ -585,12 +516,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   auto compute_step = [&](int u, const lds_u8* slot) {
     const int vch = step_vch(u);
     if (HEAT != kNoHeat && kh == 0 && pend_j >= 0) write_pending();
-    if (VIRT) {
-      // keys past n_k carry weight 0 (the table is padded), so no mask
-      if (vch > 32 * kh) vstep(slot, frag, c, vwt, u * kHalf + 32 * kh, hi, ref2, w);
-    } else if (vch > 32 * kh) {
-      hstep<HEAT, PV>(slot, frag, c, vch, kh, hi, w);
-    }
+    if (vch > 32 * kh) hstep<HEAT, PV>(slot, frag, c, vch, kh, hi, w);
     if (HEAT != kNoHeat) {
       const int32_t word = step_word(u);
       if (word & kTileEnd) flush_tile((word >> 7 & 0x7FFFFF) / kTile);
@@ -638,37 +564,24 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   const float m1 = ml[qg * 64 + li], l1 = ml[qg * 64 + 32 + li];
   const float m = fmaxf(w.m_run, m1);
   const float mu = m == -INFINITY ? 0.f : m;
-  // compensation: both halves share the fixed reference, so they add; the
-  // kept output is num / den over the kept keys with den = 1 at that
-  // reference, hence out = (o_kept + num) / (1 + den)
-  const float a0 = VIRT ? 1.f : __builtin_amdgcn_exp2f(w.m_run - mu);
-  const float a1 = VIRT ? 1.f : __builtin_amdgcn_exp2f(m1 - mu);
+  const float a0 = __builtin_amdgcn_exp2f(w.m_run - mu);
+  const float a1 = __builtin_amdgcn_exp2f(m1 - mu);
   const float l = w.l_run * a0 + l1 * a1;
   const bool row_real = DENSE ? (qrow < p.used) : true;
-  const float inv = VIRT ? 1.f / (1.f + l) : (l > 0.f && row_real) ? 1.f / l : 0.f;
+  const float inv = (l > 0.f && row_real) ? 1.f / l : 0.f;
   if (qrow >= p.q_rows) return;  // dense mode: rows past seq_len do not exist
   uint16_t* orow = p.out + qrow * p.os + head * p.oh;
-  const uint16_t* krow = VIRT ? p.o_kept + qrow * p.oks + head * p.okh : nullptr;
 #pragma unroll
   for (int dt = 0; dt < (PV ? 4 : 0); ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float v4[4];
       const int d = 32 * dt + 8 * g + 4 * hi;
-      float kept4[4] = {0.f, 0.f, 0.f, 0.f};
-      if (VIRT) {
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 kv = *reinterpret_cast<const u32x2*>(krow + d);
-        kept4[0] = bf16_to_f32(kv[0] & 0xffffu);
-        kept4[1] = bf16_to_f32(kv[0] >> 16);
-        kept4[2] = bf16_to_f32(kv[1] & 0xffffu);
-        kept4[3] = bf16_to_f32(kv[1] >> 16);
-      }
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int e = 4 * g + rr;
         const float o1 = red[(dt * 16 + e) * 64 + lane];
-        v4[rr] = (kept4[rr] + w.o[dt][e] * a0 + o1 * a1) * inv;
+        v4[rr] = (w.o[dt][e] * a0 + o1 * a1) * inv;
       }
       uint32_t w0 = pack_bf16x2(v4[0], v4[1]), w1 = pack_bf16x2(v4[2], v4[3]);
       typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -813,10 +726,42 @@ __device__ __forceinline__ void sstep(const lds_u8* slot, const HFrag& fa, const
   if (TWO) sub_pv(slot, fb, kb, w);
 }
 
+// One 32-key sub-block of a compensation step (the virtual keys of key
+// tiles key0 .. key0 + 31): p = exp2(s c - ref2) where the tile's weight
+// (its real row count if dropped, else 0) is positive, den += p * weight,
+// O^T += V^T P^T.
+__device__ __forceinline__ void sub_virtual(const lds_u8* slot, const HFrag& f, float c,
+                                            const float* wt, int key0, int hi, float ref2,
+                                            WaveState& w) {
+  const f32x16 s = sub_scores(slot, f, w, 32, hi);
+  float ps[16], den = 0.f;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const f32x4 ww = *reinterpret_cast<const f32x4*>(wt + key0 + 8 * g + 4 * hi);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const float x = ww[m] > 0.f ? __builtin_amdgcn_exp2f(fmaf(s[4 * g + m], c, -ref2)) : 0.f;
+      ps[4 * g + m] = x;
+      den = fmaf(x, ww[m], den);
+    }
+  }
+  w.l_run += den;
+  u32x4 pk[2];
+  pack_probs(ps, pk);
+  sub_pv(slot, f, pk, w);
+}
+
+// VIRT: the zero-order compensation walk. Step u is virtual keys (tile
+// summaries) 64 u .. 64 u + 63 of all n_k tiles, in order; the reference is
+// the row's fixed lse_kept instead of an online max, each key is weighted
+// by its tile's dropped real-row count, and the epilogue adds o_kept and
+// divides by 1 + den.
+template <bool VIRT>
 __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[2][kSlotBytes];
-  __shared__ uint16_t steps[2 * kMaxBlocks];
-  __shared__ uint8_t tvc[kMaxBlocks];
+  __shared__ uint16_t steps[VIRT ? 1 : 2 * kMaxBlocks];
+  __shared__ uint8_t tvc[VIRT ? 1 : kMaxBlocks];
+  __shared__ __attribute__((aligned(16))) float vwt[VIRT ? kMaxBlocks + kHalf : 1];
   __shared__ int32_t step_total;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -825,45 +770,57 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   const int64_t head = item / p.n_q_tiles;
   const int64_t r = item % p.n_q_tiles;
   const int64_t qrow = r * kTile + 32 * wave + li;
-
-  // Step list: full-list tiles as two unmasked halves, then the first
-  // halves of the partial-list tiles, then their second halves (those with
-  // more than 64 valid keys), each in list order (ballot-ranked, so the
-  // summation order is deterministic); valid counts in a byte table.
   const int nk = (int)p.n_k_tiles;
-  for (int j = tid; j < nk; j += kThreads2) tvc[j] = (uint8_t)min(max(p.valid_count[j], 0), kTile);
-  const int64_t li_ = head * p.n_q_tiles + r;
-  const int ld = (int)p.list_ld;
-  const int nf = min(max(p.full_cnt[li_], 0), min(ld, kMaxBlocks));
-  const int np = min(max(p.part_cnt[li_], 0), min(ld, kMaxBlocks - nf));
-  const int32_t* fl = p.full_idx + li_ * p.list_ld;
-  const int32_t* pl = p.part_idx + li_ * p.list_ld;
-  for (int i = tid; i < nf; i += kThreads2) {
-    const int32_t j = fl[i];
-    const bool ok = j >= 0 && j < nk;
-    steps[2 * i] = ok ? (uint16_t)((j << 2) | 1) : kVoidStep;
-    steps[2 * i + 1] = ok ? (uint16_t)((j << 2) | 3) : kVoidStep;
-  }
-  if (wave == 0) {
-    int h1 = 0;
-    for (int i0 = 0; i0 < np; i0 += 64) {
-      const int i = i0 + lane;
-      int vc = 0;
-      int32_t j = -1;
-      if (i < np) {
-        j = pl[i];
-        const bool ok = j >= 0 && j < nk;
-        if (ok) vc = min(max(p.valid_count[j], 0), kTile);
-        steps[2 * nf + i] = ok ? (uint16_t)(j << 2) : kVoidStep;
-      }
-      const bool two = i < np && vc > kHalf;
-      const uint64_t bal = __ballot(two);
-      const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
-      if (two) steps[2 * nf + np + h1 + rank] = (uint16_t)((j << 2) | 2);
-      h1 += __builtin_popcountll(bal);
+
+  if (VIRT) {
+    // weights of virtual keys 0 .. n_k - 1, padded with zeros to whole steps
+    const int padded = (nk + kHalf - 1) / kHalf * kHalf;
+    const uint8_t* keep_row = p.keep + (head * p.n_q_tiles + r) * p.n_k_tiles;
+    for (int j = tid; j < padded; j += kThreads2) {
+      float wj = 0.f;
+      if (j < nk && keep_row[j] == 0) wj = (float)min(max(p.valid_count[j], 0), kTile);
+      vwt[j] = wj;
     }
-    if (lane == 0) step_total = 2 * nf + np + h1;
+    if (tid == 0) step_total = padded / kHalf;
+  } else {
+    // Step list: full-list tiles as two unmasked halves, then the first
+    // halves of the partial-list tiles, then their second halves (those with
+    // more than 64 valid keys), each in list order (ballot-ranked, so the
+    // summation order is deterministic); valid counts in a byte table.
+    for (int j = tid; j < nk; j += kThreads2) tvc[j] = (uint8_t)min(max(p.valid_count[j], 0), kTile);
+    const int64_t li_ = head * p.n_q_tiles + r;
+    const int ld = (int)p.list_ld;
+    const int nf = min(max(p.full_cnt[li_], 0), min(ld, kMaxBlocks));
+    const int np = min(max(p.part_cnt[li_], 0), min(ld, kMaxBlocks - nf));
+    const int32_t* fl = p.full_idx + li_ * p.list_ld;
+    const int32_t* pl = p.part_idx + li_ * p.list_ld;
+    for (int i = tid; i < nf; i += kThreads2) {
+      const int32_t j = fl[i];
+      const bool ok = j >= 0 && j < nk;
+      steps[2 * i] = ok ? (uint16_t)((j << 2) | 1) : kVoidStep;
+      steps[2 * i + 1] = ok ? (uint16_t)((j << 2) | 3) : kVoidStep;
+    }
+    if (wave == 0) {
+      int h1 = 0;
+      for (int i0 = 0; i0 < np; i0 += 64) {
+        const int i = i0 + lane;
+        int vc = 0;
+        int32_t j = -1;
+        if (i < np) {
+          j = pl[i];
+          const bool ok = j >= 0 && j < nk;
+          if (ok) vc = min(max(p.valid_count[j], 0), kTile);
+          steps[2 * nf + i] = ok ? (uint16_t)(j << 2) : kVoidStep;
+        }
+        const bool two = i < np && vc > kHalf;
+        const uint64_t bal = __ballot(two);
+        const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+        if (two) steps[2 * nf + np + h1 + rank] = (uint16_t)((j << 2) | 2);
+        h1 += __builtin_popcountll(bal);
+      }
+      if (lane == 0) step_total = 2 * nf + np + h1;
+    }
   }
 
   WaveState w;
@@ -878,11 +835,22 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     for (int e = 0; e < 16; ++e) w.o[dt][e] = 0.f;
   w.m_run = -INFINITY;
   w.l_run = 0.f;
-  __syncthreads();  // step list, valid counts and step count ready
+  // compensation: the row's fixed reference (0 for a row that kept nothing)
+  float ref2 = 0.f;
+  if (VIRT) {
+    const float lk = p.lse_kept[head * p.lk_h + qrow * p.lk_s];
+    ref2 = (lk > -INFINITY && lk < INFINITY) ? lk * 1.4426950408889634f : 0.f;
+  }
+  __syncthreads();  // step list (or weights), valid counts and step count ready
   const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
 
   // (first key row, valid keys) of step u
   auto decode = [&](int u, int64_t& row0, int& vch) {
+    if (VIRT) {
+      row0 = (int64_t)u * kHalf;
+      vch = min(nk - u * kHalf, kHalf);
+      return;
+    }
     const int e = __builtin_amdgcn_readfirstlane(steps[u]);
     if (e == kVoidStep) {
       row0 = 0;
@@ -905,6 +873,20 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     decode(u, row0, vch);
     const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
     const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
+    if (VIRT && vch < kHalf) {
+      // the last step of the summaries: rows past n_k do not exist, so
+      // every lane reads a row below vch (the extra rows carry weight 0)
+      const int lr = lane >> 4, pc = lane & 15;
+#pragma unroll
+      for (int u4 = 0; u4 < 4; ++u4) {
+        const int seg = 4 * wave + u4, row = 4 * seg + lr, src = min(row, vch - 1);
+        const uint32_t ko = (uint32_t)((src * p.ks + ((pc ^ (row & 15)) << 3)) * 2);
+        const uint32_t vo = (uint32_t)((src * p.vs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
+        dma16(kb, ko, slot + seg * 1024);
+        dma16(vb, vo, slot + kHalfBytes + seg * 1024);
+      }
+      return;
+    }
 #pragma unroll
     for (int u4 = 0; u4 < 4; ++u4) {
       const int seg = 4 * wave + u4;
@@ -922,6 +904,12 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     VEDA_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
     if (u + 1 < n_steps) load_step(u + 1, nxt);
+    if (VIRT) {
+      // keys past n_k carry weight 0 (the table is padded), so no mask
+      sub_virtual(cur, fa, c, vwt, u * kHalf, hi, ref2, w);
+      sub_virtual(cur, fb, c, vwt, u * kHalf + 32, hi, ref2, w);
+      return;
+    }
     int64_t row0;
     int vch;
     decode(u, row0, vch);
@@ -936,20 +924,33 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   }
 
   const float l = half_swap_sum(w.l_run);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  // compensation: the kept output is num / den over the kept keys with
+  // den = 1 at the reference, hence out = (o_kept + num) / (1 + den)
+  const float inv = VIRT ? 1.f / (1.f + l) : l > 0.f ? 1.f / l : 0.f;
   uint16_t* orow = p.out + qrow * p.os + head * p.oh;
+  const uint16_t* krow = VIRT ? p.o_kept + qrow * p.oks + head * p.okh : nullptr;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int e = 4 * g;
       const int d = 32 * dt + 8 * g + 4 * hi;
-      uint32_t w0 = pack_bf16x2(w.o[dt][e] * inv, w.o[dt][e + 1] * inv);
-      uint32_t w1 = pack_bf16x2(w.o[dt][e + 2] * inv, w.o[dt][e + 3] * inv);
       typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      float kept4[4] = {0.f, 0.f, 0.f, 0.f};
+      if (VIRT) {
+        const u32x2 kv = *reinterpret_cast<const u32x2*>(krow + d);
+        kept4[0] = bf16_to_f32(kv[0] & 0xffffu);
+        kept4[1] = bf16_to_f32(kv[0] >> 16);
+        kept4[2] = bf16_to_f32(kv[1] & 0xffffu);
+        kept4[3] = bf16_to_f32(kv[1] >> 16);
+      }
+      float v4[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) v4[m] = (VIRT ? kept4[m] + w.o[dt][e + m] : w.o[dt][e + m]) * inv;
+      uint32_t w0 = pack_bf16x2(v4[0], v4[1]), w1 = pack_bf16x2(v4[2], v4[3]);
       *reinterpret_cast<u32x2*>(orow + d) = u32x2{w0, w1};
     }
-  if (p.lse != nullptr && hi == 0)
+  if (!VIRT && p.lse != nullptr && hi == 0)
     p.lse[head * p.lse_sh + qrow * p.lse_ss] =
         l > 0.f ? (w.m_run + __log2f(l)) * kLn2 : -INFINITY;
 }
@@ -1005,7 +1006,7 @@ extern "C" int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t 
   p.os = o_stride_s; p.oh = o_stride_h;
   p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  sfwd_kernel<<<(unsigned)items, kThreads2, 0, s>>>(p);
+  sfwd_kernel<false><<<(unsigned)items, kThreads2, 0, s>>>(p);
   return check_launch("veda_block_sparse_fwd");
 }
 
@@ -1150,6 +1151,6 @@ extern "C" int veda_zero_order_compensation(
   p.oks = ok_stride_s; p.okh = ok_stride_h;
   p.lse_kept = lse_kept; p.lk_h = lse_stride_h; p.lk_s = lse_stride_s;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hfwd_kernel<kVirtual, kNoHeat, true><<<(unsigned)items, kThreads, 0, s>>>(p);
+  sfwd_kernel<true><<<(unsigned)items, kThreads2, 0, s>>>(p);
   return check_launch("veda_zero_order_compensation");
 }
