@@ -218,6 +218,13 @@ def suite(reps: int = 5) -> dict:
     res['compensation_c2'] = _mfma(ms_c, 4.0 * c['qt'].shape[0] * n * D * HEADS)
     res['compensation_c2']['vs_sparse_fwd'] = round((ms + ms_c) / ms, 3)
     del o_kept, lse_kept
+    # the same in one pass (compensation_triton.attention): kept blocks and
+    # virtual keys in one online softmax; summaries included, lists prebuilt
+    ms_f = _median_ms(lambda: kernels.compensated_attention(c['qt'], c['kt'], c['vt'], c['mask'],
+                                                            lay, c['lists']), reps)
+    res['compensated_attention_c2'] = _mfma(ms_f, 4.0 * 128 * 128 * D * kept
+                                            + 4.0 * c['qt'].shape[0] * n * D * HEADS)
+    res['compensated_attention_c2']['vs_sparse_fwd'] = round(ms_f / ms, 3)
     ms = _median_ms(lambda: kernels.dense_attention(q, c['k'], v, used, return_lse=True), 3)
     res['dense_fwd_lse_c2'] = _mfma(ms, 4.0 * used * used * HEADS * D)
     del c, outbuf, fq, fk

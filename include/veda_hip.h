@@ -282,6 +282,33 @@ int veda_zero_order_compensation(const void* o_kept, int64_t ok_stride_s,
                                  int64_t o_stride_h, void* stream);
 
 /*
+ * Compensated block-sparse attention in one pass
+ * (miowtion/kernels/compensation_triton.py:228-258 attention: the FA4
+ * forward over the kept blocks, then compensate): the listed blocks
+ * (full_* / part_*, as for veda_block_sparse_fwd) and then, for every key
+ * tile j with keep[h, i, j] == 0 and valid_count[j] > 0, one virtual key
+ * kc[j] with value vc[j] and weight valid_count[j] (the tile summaries of
+ * veda_tile_summaries), all inside one online softmax: out = (sum over
+ * kept keys of p v + sum over dropped tiles of p vc) / (sum over kept keys
+ * of p + sum of p valid_count). A row that kept nothing gets the
+ * reference's unit mass at reference 0 (out = num / (1 + den)). keep:
+ * bytes [n_heads, n_q_tiles, n_k_tiles], the kept-block mask with kv_ok
+ * applied. Shapes and strides as veda_block_sparse_fwd and
+ * veda_zero_order_compensation.
+ */
+int veda_compensated_attention(const void* q, int64_t q_stride_s, int64_t q_stride_h,
+                               const void* k, int64_t k_stride_s, int64_t k_stride_h,
+                               const void* v, int64_t v_stride_s, int64_t v_stride_h,
+                               int64_t n_heads, int64_t head_dim, int64_t n_q_tiles,
+                               int64_t n_k_tiles, const int32_t* full_cnt,
+                               const int32_t* full_idx, const int32_t* part_cnt,
+                               const int32_t* part_idx, int64_t list_ld, const void* kc,
+                               const void* vc, int64_t c_stride_s, int64_t c_stride_h,
+                               const uint8_t* keep, const int32_t* valid_count, float scale,
+                               void* out, int64_t o_stride_s, int64_t o_stride_h,
+                               void* stream);
+
+/*
  * Block-sparse attention backward: the gradients of veda_block_sparse_fwd
  * (FA4's backward with the Q-direction lists, reached through
  * miowtion/kernels/fa4.py:340-373 -> fa4_sm8x/interface.py:3722-3790

@@ -45,6 +45,9 @@ SIGNATURES: dict[str, list] = {
                               _P, _I, _I, _P, _I, _I, _I, _I, _I, _I,
                               _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _F,
                               _P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _P],
+    'veda_compensated_attention': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I,
+                                   _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P, _F,
+                                   _P, _I, _I, _P],
     'veda_predictor_embed': [_P, _I, _I, _I, _P, _C, _P, _I, _P, _I, _C, _P, _P],
     'veda_predictor_logits': [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _C, _P, _P],
 }

@@ -202,11 +202,9 @@ class SparseStudent:
             lists = kernels.index_lists(block_mask, tile_layout)
             cfg = self.clip.config
             if cfg.zero_order_compensation or cfg.triton_compensation:
-                o_kept, lse_kept = kernels.block_sparse_attention_lists(
-                    q_tiles, k_tiles, v_tiles, lists, tile_layout, return_lse=True)
-                o_tiles = kernels.zero_order_compensation(
-                    o_kept, lse_kept, q_tiles, k_tiles, v_tiles,
-                    block_mask & tile_layout.kv_ok[None, None, :], tile_layout)
+                # the lists already hold only kv_ok tiles (index_lists applies it)
+                o_tiles = kernels.compensated_attention(q_tiles, k_tiles, v_tiles, block_mask,
+                                                        tile_layout, lists)
             else:
                 o_tiles = kernels.block_sparse_attention_lists(q_tiles, k_tiles, v_tiles, lists,
                                                                tile_layout)

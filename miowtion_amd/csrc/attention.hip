@@ -69,14 +69,19 @@ struct FwdParams {
   // per-(key tile, query row) block statistic [H'][n_k][items * 128] in
   // log2 units (block log-sum-exp for heat 'sum', block max for 'max').
   const int64_t* q_tiles;
-  int64_t q_tiles_held;
-  // Virtual-key walk (zero-order compensation) only: the kept-block mask
-  // [H'][items][n_k] (bytes), the kept output o_kept and its LSE lse_kept.
+  int64_t q_tiles_held;  // tiles q holds; an item whose q_tiles entry is outside reads zeros
+  // Virtual keys (zero-order compensation) only: the kept-block mask
+  // [H'][items][n_k] (bytes), the tile summaries kc / vc ([n_k][H'][D],
+  // strides cs, ch), and for the compensation of a given output, that
+  // output o_kept and its LSE lse_kept.
   const uint8_t* keep;
+  const uint16_t* kc;
+  const uint16_t* vc;
+  int64_t cs, ch;
   const uint16_t* o_kept;
   int64_t oks, okh;
   const float* lse_kept;
-  int64_t lk_h, lk_s;  // tiles q holds; an item whose q_tiles entry is outside reads zeros
+  int64_t lk_h, lk_s;
   float* part;
   int64_t part_sh, part_st;
 };
@@ -730,20 +735,27 @@ __device__ __forceinline__ void sstep(const lds_u8* slot, const HFrag& fa, const
 // tiles key0 .. key0 + 31): p = exp2(s c - ref2) where the tile's weight
 // (its real row count if dropped, else 0) is positive, den += p * weight,
 // O^T += V^T P^T.
-__device__ __forceinline__ void sub_virtual(const lds_u8* slot, const HFrag& f, float c,
-                                            const float* wt, int key0, int hi, float ref2,
-                                            WaveState& w) {
-  const f32x16 s = sub_scores(slot, f, w, 32, hi);
-  float ps[16], den = 0.f;
+// The 16 weights of this lane's keys key0 + 8 g + 4 hi + m of a sub-block.
+__device__ __forceinline__ void sub_weights(const uint8_t* wt, int key0, int hi, float (&ww)[16]) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    const f32x4 ww = *reinterpret_cast<const f32x4*>(wt + key0 + 8 * g + 4 * hi);
+    const uint32_t w4 = *reinterpret_cast<const uint32_t*>(wt + key0 + 8 * g + 4 * hi);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const float x = ww[m] > 0.f ? __builtin_amdgcn_exp2f(fmaf(s[4 * g + m], c, -ref2)) : 0.f;
-      ps[4 * g + m] = x;
-      den = fmaf(x, ww[m], den);
-    }
+    for (int m = 0; m < 4; ++m) ww[4 * g + m] = (float)((w4 >> (8 * m)) & 0xffu);
+  }
+}
+
+__device__ __forceinline__ void sub_virtual(const lds_u8* slot, const HFrag& f, float c,
+                                            const uint8_t* wt, int key0, int hi, float ref2,
+                                            WaveState& w) {
+  const f32x16 s = sub_scores(slot, f, w, 32, hi);
+  float ww[16], ps[16], den = 0.f;
+  sub_weights(wt, key0, hi, ww);
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const float x = ww[e] > 0.f ? __builtin_amdgcn_exp2f(fmaf(s[e], c, -ref2)) : 0.f;
+    ps[e] = x;
+    den = fmaf(x, ww[e], den);
   }
   w.l_run += den;
   u32x4 pk[2];
@@ -751,17 +763,77 @@ __device__ __forceinline__ void sub_virtual(const lds_u8* slot, const HFrag& f, 
   sub_pv(slot, f, pk, w);
 }
 
-// VIRT: the zero-order compensation walk. Step u is virtual keys (tile
-// summaries) 64 u .. 64 u + 63 of all n_k tiles, in order; the reference is
-// the row's fixed lse_kept instead of an online max, each key is weighted
-// by its tile's dropped real-row count, and the epilogue adds o_kept and
-// divides by 1 + den.
-template <bool VIRT>
+// One step of 64 virtual keys inside the online softmax (compensated
+// attention): as sstep, with each key weighted by its tile's dropped
+// real-row count (the denominator gains p * weight; the value is the
+// tile's sum of V) and weight-0 keys masked out of the max.
+__device__ __forceinline__ void sstep_virtual(const lds_u8* slot, const HFrag& fa,
+                                              const HFrag& fb, float c, const uint8_t* wt,
+                                              int key0, int hi, WaveState& w) {
+  f32x16 sa = sub_scores(slot, fa, w, 32, hi);
+  f32x16 sb = sub_scores(slot, fb, w, 32, hi);
+  // weights stay packed, 4 per word (byte e % 4 of word e / 4 is key
+  // 8 (e / 4) + 4 hi + e % 4 of the sub-block)
+  uint32_t wa[4], wb[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    wa[g] = *reinterpret_cast<const uint32_t*>(wt + key0 + 8 * g + 4 * hi);
+    wb[g] = *reinterpret_cast<const uint32_t*>(wt + key0 + 32 + 8 * g + 4 * hi);
+  }
+  auto byte = [](uint32_t x, int m) { return (x >> (8 * m)) & 0xffu; };
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    sa[e] = byte(wa[e >> 2], e & 3) ? sa[e] : -INFINITY;
+    sb[e] = byte(wb[e >> 2], e & 3) ? sb[e] : -INFINITY;
+    mloc = fmaxf(mloc, fmaxf(sa[e], sb[e]));
+  }
+  mloc = half_swap_max(mloc) * c;
+  const float m_new = mloc > w.m_run + kRescaleSlack ? mloc : w.m_run;
+  const float mu = m_new == -INFINITY ? 0.f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(w.m_run - mu);
+  w.m_run = m_new;
+  float pa[16], pb[16], lsum = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    pa[e] = __builtin_amdgcn_exp2f(fmaf(sa[e], c, -mu));
+    pb[e] = __builtin_amdgcn_exp2f(fmaf(sb[e], c, -mu));
+    lsum = fmaf(pa[e], (float)byte(wa[e >> 2], e & 3), fmaf(pb[e], (float)byte(wb[e >> 2], e & 3), lsum));
+  }
+  w.l_run = fmaf(w.l_run, alpha, lsum);
+  u32x4 ka[2], kb[2];
+  pack_probs(pa, ka);
+  pack_probs(pb, kb);
+  if (__any(alpha != 1.f)) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) w.o[dt][e] *= alpha;
+  }
+  sub_pv(slot, fa, ka, w);
+  sub_pv(slot, fb, kb, w);
+}
+
+// Modes: kSparse walks the block lists. kVirtualOnly is the zero-order
+// compensation of a given output: step u is virtual keys (tile summaries)
+// 64 u .. 64 u + 63 of all n_k tiles, the reference is the row's fixed
+// lse_kept instead of an online max, each key is weighted by its tile's
+// dropped real-row count, and the epilogue adds o_kept and divides by
+// 1 + den. kSparseComp is compensated attention in one pass: the list steps,
+// then the virtual-key steps inside the same online softmax (a row that kept
+// nothing first gets the reference's unit mass at reference 0, with value 0,
+// so it ends as num / (1 + den) as well).
+enum SparseMode { kSparse = 0, kVirtualOnly = 1, kSparseComp = 2 };
+
+template <int MODE>
 __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
+  constexpr bool LISTS = MODE != kVirtualOnly;  // walks the block lists
+  constexpr bool VKEYS = MODE != kSparse;       // walks the virtual keys
   __shared__ __attribute__((aligned(1024))) uint8_t ring[2][kSlotBytes];
-  __shared__ uint16_t steps[VIRT ? 1 : 2 * kMaxBlocks];
-  __shared__ uint8_t tvc[VIRT ? 1 : kMaxBlocks];
-  __shared__ __attribute__((aligned(16))) float vwt[VIRT ? kMaxBlocks + kHalf : 1];
+  __shared__ uint16_t steps[LISTS ? 2 * kMaxBlocks : 1];
+  __shared__ uint8_t tvc[LISTS ? kMaxBlocks : 1];
+  // virtual keys: per key tile, its real row count if dropped, else 0
+  __shared__ __attribute__((aligned(16))) uint8_t vwt[VKEYS ? kMaxBlocks + kHalf : 4];
   __shared__ int32_t step_total;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -772,16 +844,18 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   const int64_t qrow = r * kTile + 32 * wave + li;
   const int nk = (int)p.n_k_tiles;
 
-  if (VIRT) {
+  const int n_virt = VKEYS ? (nk + kHalf - 1) / kHalf : 0;
+  if (VKEYS) {
     // weights of virtual keys 0 .. n_k - 1, padded with zeros to whole steps
-    const int padded = (nk + kHalf - 1) / kHalf * kHalf;
     const uint8_t* keep_row = p.keep + (head * p.n_q_tiles + r) * p.n_k_tiles;
-    for (int j = tid; j < padded; j += kThreads2) {
-      float wj = 0.f;
-      if (j < nk && keep_row[j] == 0) wj = (float)min(max(p.valid_count[j], 0), kTile);
-      vwt[j] = wj;
+    for (int j = tid; j < n_virt * kHalf; j += kThreads2) {
+      int wj = 0;
+      if (j < nk && keep_row[j] == 0) wj = min(max(p.valid_count[j], 0), kTile);
+      vwt[j] = (uint8_t)wj;
     }
-    if (tid == 0) step_total = padded / kHalf;
+  }
+  if (!LISTS) {
+    if (tid == 0) step_total = 0;
   } else {
     // Step list: full-list tiles as two unmasked halves, then the first
     // halves of the partial-list tiles, then their second halves (those with
@@ -835,20 +909,23 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     for (int e = 0; e < 16; ++e) w.o[dt][e] = 0.f;
   w.m_run = -INFINITY;
   w.l_run = 0.f;
-  // compensation: the row's fixed reference (0 for a row that kept nothing)
+  // compensation of a given output: the row's fixed reference (0 for a row
+  // that kept nothing)
   float ref2 = 0.f;
-  if (VIRT) {
+  if (MODE == kVirtualOnly) {
     const float lk = p.lse_kept[head * p.lk_h + qrow * p.lk_s];
     ref2 = (lk > -INFINITY && lk < INFINITY) ? lk * 1.4426950408889634f : 0.f;
   }
-  __syncthreads();  // step list (or weights), valid counts and step count ready
-  const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
+  __syncthreads();  // step list, weights, valid counts and list step count ready
+  const int n_lsteps = __builtin_amdgcn_readfirstlane(step_total);
+  const int n_steps = n_lsteps + n_virt;
 
-  // (first key row, valid keys) of step u
+  // (first key row, valid keys) of step u; steps n_lsteps .. are virtual
   auto decode = [&](int u, int64_t& row0, int& vch) {
-    if (VIRT) {
-      row0 = (int64_t)u * kHalf;
-      vch = min(nk - u * kHalf, kHalf);
+    if (VKEYS && u >= n_lsteps) {
+      const int v = u - n_lsteps;
+      row0 = (int64_t)v * kHalf;
+      vch = min(nk - v * kHalf, kHalf);
       return;
     }
     const int e = __builtin_amdgcn_readfirstlane(steps[u]);
@@ -866,27 +943,38 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   const uint16_t* vbase = p.v + head * p.vh;
   const float c = p.scale_log2;
   const SDma dma = sdma_offsets(p.ks, p.vs, wave, lane);
+  const SDma cdma = sdma_offsets(VKEYS ? p.cs : 0, VKEYS ? p.cs : 0, wave, lane);  // summaries
   const HFrag fa = hfrag_offsets(0, lane), fb = hfrag_offsets(1, lane);
   auto load_step = [&](int u, lds_u8* slot) {
     int64_t row0;
     int vch;
     decode(u, row0, vch);
-    const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
-    const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
-    if (VIRT && vch < kHalf) {
-      // the last step of the summaries: rows past n_k do not exist, so
-      // every lane reads a row below vch (the extra rows carry weight 0)
+    if (VKEYS && u >= n_lsteps) {
+      // summaries; in the last step rows past n_k do not exist, so every
+      // lane reads a row below vch (the extra rows carry weight 0)
+      const char* kb = reinterpret_cast<const char*>(p.kc + head * p.ch + row0 * p.cs);
+      const char* vb = reinterpret_cast<const char*>(p.vc + head * p.ch + row0 * p.cs);
+      if (vch == kHalf) {
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+          dma16(kb, cdma.k[u4], slot + (4 * wave + u4) * 1024);
+          dma16(vb, cdma.v[u4], slot + kHalfBytes + (4 * wave + u4) * 1024);
+        }
+        return;
+      }
       const int lr = lane >> 4, pc = lane & 15;
 #pragma unroll
       for (int u4 = 0; u4 < 4; ++u4) {
         const int seg = 4 * wave + u4, row = 4 * seg + lr, src = min(row, vch - 1);
-        const uint32_t ko = (uint32_t)((src * p.ks + ((pc ^ (row & 15)) << 3)) * 2);
-        const uint32_t vo = (uint32_t)((src * p.vs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
+        const uint32_t ko = (uint32_t)((src * p.cs + ((pc ^ (row & 15)) << 3)) * 2);
+        const uint32_t vo = (uint32_t)((src * p.cs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
         dma16(kb, ko, slot + seg * 1024);
         dma16(vb, vo, slot + kHalfBytes + seg * 1024);
       }
       return;
     }
+    const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
+    const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
 #pragma unroll
     for (int u4 = 0; u4 < 4; ++u4) {
       const int seg = 4 * wave + u4;
@@ -900,35 +988,85 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   // Step u: wait for its own loads (the only ones in flight), barrier (all
   // waves' loads of step u are in LDS and all are done reading the other
   // slot), issue step u + 1 into the other slot, compute step u.
-  auto run = [&](int u, lds_u8* cur, lds_u8* nxt) {
+  auto begin_step = [&](int u, lds_u8* nxt) {
     VEDA_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
     if (u + 1 < n_steps) load_step(u + 1, nxt);
-    if (VIRT) {
-      // keys past n_k carry weight 0 (the table is padded), so no mask
-      sub_virtual(cur, fa, c, vwt, u * kHalf, hi, ref2, w);
-      sub_virtual(cur, fb, c, vwt, u * kHalf + 32, hi, ref2, w);
-      return;
-    }
+  };
+  auto list_step = [&](int u, const lds_u8* cur) {
     int64_t row0;
     int vch;
     decode(u, row0, vch);
     if (vch > 32) sstep<true>(cur, fa, fb, c, vch, hi, w);
     else if (vch > 0) sstep<false>(cur, fa, fb, c, vch, hi, w);
   };
+  auto virtual_step = [&](int u, const lds_u8* cur) {
+    // keys past n_k carry weight 0 (the table is padded), so no mask
+    const int key0 = (u - n_lsteps) * kHalf;
+    if (MODE == kVirtualOnly) {
+      sub_virtual(cur, fa, c, vwt, key0, hi, ref2, w);
+      sub_virtual(cur, fb, c, vwt, key0 + 32, hi, ref2, w);
+    } else {
+      sstep_virtual(cur, fa, fb, c, vwt, key0, hi, w);
+    }
+  };
   if (n_steps > 0) load_step(0, s0);
-  for (int u = 0; u < n_steps; u += 2) {
-    run(u, s0, s1);
-    if (u + 1 >= n_steps) break;
-    run(u + 1, s1, s0);
+  if (!VKEYS) {
+    for (int u = 0; u < n_steps; u += 2) {
+      begin_step(u, s1);
+      list_step(u, s0);
+      if (u + 1 >= n_steps) break;
+      begin_step(u + 1, s0);
+      list_step(u + 1, s1);
+    }
+  } else {
+    // the list steps, then the virtual steps, as two loops (each with its
+    // own register peak); step u is in slot u % 2. Both loops are unrolled
+    // by two so that every fragment read has a constant slot address.
+    int u = 0;
+    for (; u + 1 < n_lsteps; u += 2) {
+      begin_step(u, s1);
+      list_step(u, s0);
+      begin_step(u + 1, s0);
+      list_step(u + 1, s1);
+    }
+    if (u < n_lsteps) {
+      begin_step(u, s1);
+      list_step(u, s0);
+      ++u;
+    }
+    if (MODE == kSparseComp) {
+      // a row that kept nothing: the reference's unit mass at reference 0
+      // (a select, not a branch: the condition is per row)
+      const bool empty = half_swap_sum(w.l_run) == 0.f;
+      w.m_run = empty ? 0.f : w.m_run;
+      w.l_run = empty ? (hi == 0 ? 1.f : 0.f) : w.l_run;
+    }
+    if (u & 1) {  // odd number of list steps: one virtual step from slot 1
+      if (u < n_steps) {
+        begin_step(u, s0);
+        virtual_step(u, s1);
+        ++u;
+      }
+    }
+    for (; u + 1 < n_steps; u += 2) {
+      begin_step(u, s1);
+      virtual_step(u, s0);
+      begin_step(u + 1, s0);
+      virtual_step(u + 1, s1);
+    }
+    if (u < n_steps) {
+      begin_step(u, s1);
+      virtual_step(u, s0);
+    }
   }
 
   const float l = half_swap_sum(w.l_run);
   // compensation: the kept output is num / den over the kept keys with
   // den = 1 at the reference, hence out = (o_kept + num) / (1 + den)
-  const float inv = VIRT ? 1.f / (1.f + l) : l > 0.f ? 1.f / l : 0.f;
+  const float inv = MODE == kVirtualOnly ? 1.f / (1.f + l) : l > 0.f ? 1.f / l : 0.f;
   uint16_t* orow = p.out + qrow * p.os + head * p.oh;
-  const uint16_t* krow = VIRT ? p.o_kept + qrow * p.oks + head * p.okh : nullptr;
+  const uint16_t* krow = MODE == kVirtualOnly ? p.o_kept + qrow * p.oks + head * p.okh : nullptr;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -937,7 +1075,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       const int d = 32 * dt + 8 * g + 4 * hi;
       typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
       float kept4[4] = {0.f, 0.f, 0.f, 0.f};
-      if (VIRT) {
+      if (MODE == kVirtualOnly) {
         const u32x2 kv = *reinterpret_cast<const u32x2*>(krow + d);
         kept4[0] = bf16_to_f32(kv[0] & 0xffffu);
         kept4[1] = bf16_to_f32(kv[0] >> 16);
@@ -946,11 +1084,12 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       }
       float v4[4];
 #pragma unroll
-      for (int m = 0; m < 4; ++m) v4[m] = (VIRT ? kept4[m] + w.o[dt][e + m] : w.o[dt][e + m]) * inv;
+      for (int m = 0; m < 4; ++m)
+        v4[m] = (MODE == kVirtualOnly ? kept4[m] + w.o[dt][e + m] : w.o[dt][e + m]) * inv;
       uint32_t w0 = pack_bf16x2(v4[0], v4[1]), w1 = pack_bf16x2(v4[2], v4[3]);
       *reinterpret_cast<u32x2*>(orow + d) = u32x2{w0, w1};
     }
-  if (!VIRT && p.lse != nullptr && hi == 0)
+  if (MODE == kSparse && p.lse != nullptr && hi == 0)
     p.lse[head * p.lse_sh + qrow * p.lse_ss] =
         l > 0.f ? (w.m_run + __log2f(l)) * kLn2 : -INFINITY;
 }
@@ -1006,8 +1145,60 @@ extern "C" int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t 
   p.os = o_stride_s; p.oh = o_stride_h;
   p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  sfwd_kernel<false><<<(unsigned)items, kThreads2, 0, s>>>(p);
+  sfwd_kernel<kSparse><<<(unsigned)items, kThreads2, 0, s>>>(p);
   return check_launch("veda_block_sparse_fwd");
+}
+
+extern "C" int veda_compensated_attention(
+    const void* q, int64_t q_stride_s, int64_t q_stride_h, const void* k, int64_t k_stride_s,
+    int64_t k_stride_h, const void* v, int64_t v_stride_s, int64_t v_stride_h, int64_t n_heads,
+    int64_t head_dim, int64_t n_q_tiles, int64_t n_k_tiles, const int32_t* full_cnt,
+    const int32_t* full_idx, const int32_t* part_cnt, const int32_t* part_idx, int64_t list_ld,
+    const void* kc, const void* vc, int64_t c_stride_s, int64_t c_stride_h, const uint8_t* keep,
+    const int32_t* valid_count, float scale, void* out, int64_t o_stride_s, int64_t o_stride_h,
+    void* stream) {
+  VEDA_REQUIRE(head_dim == kD, "compensated_attention: head_dim must be 128, got %lld",
+               (long long)head_dim);
+  VEDA_REQUIRE(n_heads >= 0 && n_q_tiles >= 0 && n_k_tiles >= 0,
+               "compensated_attention: negative size");
+  VEDA_REQUIRE(list_ld >= n_k_tiles, "compensated_attention: list_ld %lld < n_k_tiles %lld",
+               (long long)list_ld, (long long)n_k_tiles);
+  VEDA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(kc) && aligned16(vc) &&
+                   aligned16(out) && q_stride_s % 8 == 0 && q_stride_h % 8 == 0 &&
+                   k_stride_s % 8 == 0 && k_stride_h % 8 == 0 && v_stride_s % 8 == 0 &&
+                   v_stride_h % 8 == 0 && c_stride_s % 8 == 0 && c_stride_h % 8 == 0 &&
+                   o_stride_s % 4 == 0 && o_stride_h % 4 == 0,
+               "compensated_attention: rows must be 16-byte aligned");
+  VEDA_REQUIRE(2 * c_stride_s < (1 << 24), "compensated_attention: summary stride too large");
+  const int64_t items = n_heads * n_q_tiles;
+  if (items == 0) return VEDA_OK;
+  VEDA_REQUIRE(n_k_tiles >= 1 && n_k_tiles <= kMaxBlocks,
+               "compensated_attention: n_k_tiles %lld outside [1, %d]", (long long)n_k_tiles,
+               kMaxBlocks);
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.qs = q_stride_s; p.qh = q_stride_h;
+  p.ks = k_stride_s; p.kh = k_stride_h;
+  p.vs = v_stride_s; p.vh = v_stride_h;
+  p.n_heads = n_heads; p.n_q_tiles = n_q_tiles; p.n_k_tiles = n_k_tiles;
+  p.full_cnt = full_cnt; p.full_idx = full_idx;
+  p.part_cnt = part_cnt; p.part_idx = part_idx;
+  p.list_ld = list_ld;
+  p.valid_count = valid_count;
+  p.kv_rows = n_k_tiles * kTile;
+  p.q_rows = n_q_tiles * kTile;
+  p.scale_log2 = (float)((double)scale * 1.4426950408889634);
+  p.out = static_cast<uint16_t*>(out);
+  p.os = o_stride_s; p.oh = o_stride_h;
+  p.keep = keep;
+  p.kc = static_cast<const uint16_t*>(kc);
+  p.vc = static_cast<const uint16_t*>(vc);
+  p.cs = c_stride_s; p.ch = c_stride_h;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  sfwd_kernel<kSparseComp><<<(unsigned)items, kThreads2, 0, s>>>(p);
+  return check_launch("veda_compensated_attention");
 }
 
 extern "C" int veda_dense_fwd(const void* q, int64_t q_stride_s, int64_t q_stride_h,
@@ -1135,11 +1326,10 @@ extern "C" int veda_zero_order_compensation(
                kMaxBlocks);
   FwdParams p{};
   p.q = static_cast<const uint16_t*>(q);
-  p.k = static_cast<const uint16_t*>(kc);
-  p.v = static_cast<const uint16_t*>(vc);
+  p.kc = static_cast<const uint16_t*>(kc);
+  p.vc = static_cast<const uint16_t*>(vc);
+  p.cs = c_stride_s; p.ch = c_stride_h;
   p.qs = q_stride_s; p.qh = q_stride_h;
-  p.ks = c_stride_s; p.kh = c_stride_h;
-  p.vs = c_stride_s; p.vh = c_stride_h;
   p.n_heads = n_heads; p.n_q_tiles = n_q_tiles; p.n_k_tiles = n_k_tiles;
   p.valid_count = valid_count;
   p.q_rows = n_q_tiles * kTile;
@@ -1151,6 +1341,6 @@ extern "C" int veda_zero_order_compensation(
   p.oks = ok_stride_s; p.okh = ok_stride_h;
   p.lse_kept = lse_kept; p.lk_h = lse_stride_h; p.lk_s = lse_stride_s;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  sfwd_kernel<true><<<(unsigned)items, kThreads2, 0, s>>>(p);
+  sfwd_kernel<kVirtualOnly><<<(unsigned)items, kThreads2, 0, s>>>(p);
   return check_launch("veda_zero_order_compensation");
 }

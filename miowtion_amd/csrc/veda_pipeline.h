@@ -67,9 +67,11 @@ __device__ __forceinline__ float wave_reduce(float v) {
 // M0 (the LDS destination) is written inside the same statement, right
 // before its use; nothing else in these kernels uses M0 (the compiler
 // reports m0 as reserved in the clobber list and may not preserve it, which
-// is why no value in it may live across the statement).
+// is why no value in it may live across the statement). The destination is
+// wave-uniform by construction; readfirstlane states that to the compiler,
+// which otherwise may keep it in a vector register after a per-lane select.
 __device__ __forceinline__ void dma16(const char* base, uint32_t voff, const lds_u8* dst) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)dst;
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
   asm volatile(
       "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"

@@ -257,9 +257,27 @@ def zero_order_compensation(o_kept: torch.Tensor, lse_kept: torch.Tensor, q: tor
 
 
 def compensated_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                          block_mask: torch.Tensor, layout: tiling.TileLayout) -> torch.Tensor:
+                          block_mask: torch.Tensor, layout: tiling.TileLayout,
+                          lists: tuple[torch.Tensor, ...] | None = None) -> torch.Tensor:
     """Block-sparse attention over the kept blocks plus the zero-order term
-    of the dropped ones (compensation_triton.attention, :228-258)."""
+    of the dropped ones (compensation_triton.attention, :228-258), in one
+    pass: the kept blocks and then every dropped tile's virtual key go
+    through the same online softmax, so o_kept and its LSE never leave the
+    kernel. Same result as zero_order_compensation after
+    block_sparse_attention, without the bf16 rounding of o_kept between
+    them.
+
+    Args:
+        q: [R * 128, H', D] bf16 query tiles; k, v: [N, H', D] bf16 key tiles.
+        block_mask: [H', R, n] bool, True where the block is kept exactly.
+        layout: Tile layout.
+        lists: index_lists of block_mask & kv_ok, if already built.
+
+    Returns:
+        [R * 128, H', D] bf16.
+    """
     kept = block_mask & layout.kv_ok[None, None, :]
-    o_kept, lse = block_sparse_attention(q, k, v, kept, layout, return_lse=True)
-    return zero_order_compensation(o_kept, lse, q, k, v, kept, layout)
+    if lists is None:
+        lists = index_lists(kept, layout)
+    kc, vc = tile_summaries(k, v, layout)
+    return ops.compensated_attention(q, k, v, *lists, kc, vc, kept, layout.valid_count)

@@ -541,6 +541,52 @@ def _(o_kept, lse_kept, q, kc, vc, block_mask, valid_count):
     return torch.empty_like(o_kept)
 
 
+@torch.library.custom_op('veda::compensated_attention', mutates_args=())
+def compensated_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          part_cnt: torch.Tensor, part_idx: torch.Tensor, full_cnt: torch.Tensor,
+                          full_idx: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor,
+                          block_mask: torch.Tensor, valid_count: torch.Tensor) -> torch.Tensor:
+    """Block-sparse attention over the listed (kept) blocks plus the
+    zero-order term of every other non-empty key tile, in one pass
+    (compensation_triton.attention, :228-258). Lists as index_lists returns
+    them for block_mask (the kept blocks, kv_ok applied); kc / vc the tile
+    summaries."""
+    _require_gpu(q, k, v, part_cnt, part_idx, full_cnt, full_idx, kc, vc, block_mask,
+                 valid_count)
+    for name, t in (('q', q), ('k', k), ('v', v), ('kc', kc), ('vc', vc)):
+        _check_rows(name, t)
+    rq, heads, d = q.shape
+    if (d != 128 or rq % TILE or k.shape[0] % TILE or k.shape != v.shape
+            or k.shape[1:] != q.shape[1:]):
+        raise ValueError(f'bad shapes q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}')
+    r_tiles, n = rq // TILE, k.shape[0] // TILE
+    _check_lists('part', part_cnt, part_idx, heads, r_tiles, n)
+    _check_lists('full', full_cnt, full_idx, heads, r_tiles, n)
+    if part_idx.shape[3] != full_idx.shape[3]:
+        raise ValueError('the part and full lists must have equal rows')
+    if vc.shape != kc.shape or tuple(kc.shape) != (n, heads, d):
+        raise ValueError(f"kc / vc must be [{n}, {heads}, {d}]")
+    if block_mask.dtype != torch.bool or tuple(block_mask.shape) != (heads, r_tiles, n):
+        raise ValueError(f'block_mask must be bool [{heads}, {r_tiles}, {n}]')
+    if valid_count.numel() != n or valid_count.dtype != torch.int32:
+        raise ValueError(f'valid_count must be int32 [{n}]')
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    keep = block_mask.contiguous()
+    _native.call('veda_compensated_attention', q.data_ptr(), q.stride(0), q.stride(1),
+                 k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+                 heads, d, r_tiles, n, full_cnt.data_ptr(), full_idx.data_ptr(),
+                 part_cnt.data_ptr(), part_idx.data_ptr(), part_idx.shape[3], kc.data_ptr(),
+                 vc.data_ptr(), kc.stride(0), kc.stride(1), keep.data_ptr(),
+                 valid_count.contiguous().data_ptr(), 1.0 / math.sqrt(d), out.data_ptr(),
+                 out.stride(0), out.stride(1), _stream(q))
+    return out
+
+
+@compensated_attention.register_fake
+def _(q, k, v, part_cnt, part_idx, full_cnt, full_idx, kc, vc, block_mask, valid_count):
+    return torch.empty_like(q)
+
+
 # --------------------------------------------------------------------------
 # predictor (miowtion/veda/predictor.py:251-338)
 

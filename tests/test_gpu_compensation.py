@@ -69,9 +69,11 @@ def test_compensation_matches_oracle():
     _bar(got, want32)
     # the term is present: the output moved away from o_kept
     assert (got.float() - o_c.float()).abs().max() > 5e-2
-    # end to end form (kept = mask & kv_ok) gives the same bits
+    # the one-pass form (kept = mask & kv_ok) keeps o_kept in fp32: the same
+    # result up to that bf16 rounding
     both = kernels.compensated_attention(qt.cuda(), kt.cuda(), vt.cuda(), mask.cuda(), lay).cpu()
-    assert torch.equal(both, got)
+    torch.testing.assert_close(both.float(), got.float(), rtol=1e-2, atol=4e-3)
+    _bar(both, want32)
 
 
 def test_exact_when_dropped_tiles_hold_one_key():
@@ -85,6 +87,23 @@ def test_exact_when_dropped_tiles_hold_one_key():
                                         lay).cpu()
     full = oa.block_sparse_attention(qt, k_same, vt, torch.ones_like(mask), olay.valid_count)
     _bar(got, full)
+
+
+def test_one_pass_row_that_kept_nothing():
+    """A query tile whose mask row is empty: the one-pass kernel gives the
+    reference's num / (1 + den) at reference 0 (attention.py:640-650)."""
+    lay, olay, qt, kt, vt, mask = _case(3)
+    m = mask.clone()
+    m[0, 1] = False
+    m[2, 0] = False
+    got = kernels.compensated_attention(qt.cuda(), kt.cuda(), vt.cuda(), m.cuda(), lay).cpu()
+    o, lse = oa.block_sparse_attention(qt, kt, vt, m & olay.kv_ok, olay.valid_count,
+                                       return_lse=True)
+    assert torch.isinf(lse[0, 128:256]).all()
+    want = oa.zero_order_compensation(o, lse, qt, kt, vt, m & olay.kv_ok, olay.valid_count,
+                                      torch.bfloat16)
+    _bar(got, want.float())
+    _bar(got[128:256, 0], want[128:256, 0].float())
 
 
 def test_nothing_dropped_returns_o_kept():
@@ -158,3 +177,6 @@ def test_config2_sampled_query_tiles():
                                       vt_c, mask.cpu()[:, tiles], lay.valid_count.cpu(),
                                       torch.bfloat16)
     torch.testing.assert_close(got.cpu()[rows].float(), want.float(), rtol=1e-2, atol=4e-3)
+    # the one-pass form on the same inputs
+    one = kernels.compensated_attention(qt, kt, vt, mask, lay)
+    torch.testing.assert_close(one.cpu()[rows].float(), want.float(), rtol=1e-2, atol=8e-3)
