@@ -205,7 +205,8 @@ def suite(reps: int = 5) -> dict:
     dout = torch.randn(o_f.shape, generator=torch.Generator(device='cuda').manual_seed(3),
                        device='cuda').to(torch.bfloat16)
     ms_b = _median_ms(lambda: ops.block_sparse_bwd(c['qt'], c['kt'], c['vt'], o_f, dout, lse_f, None,
-                                                   *c['lists'], *lists_t, lay.valid_count), reps)
+                                                   *c['lists'], *lists_t, lay.valid_count,
+                                                   lay.n_tiles - lay.n_video_tiles), reps)
     res['sparse_bwd_c2'] = _mfma(ms_b, 10.0 * 128 * 128 * D * kept)
     res['sparse_bwd_c2']['vs_sparse_fwd'] = round(ms_b / ms, 3)
     del lists_t, o_f, lse_f, dout
@@ -310,7 +311,8 @@ def _backward(c: dict, kept: int, steps: int, warmup: int) -> int:
 
     def step():
         return ops.block_sparse_bwd(c['qt'], c['kt'], c['vt'], o, dout, lse, None, *c['lists'],
-                                    *lists_t, lay.valid_count)
+                                    *lists_t, lay.valid_count,
+                                    lay.n_tiles - lay.n_video_tiles)
 
     _log(f'bench: backward, warmup {warmup}')
     for _ in range(warmup):

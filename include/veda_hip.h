@@ -154,6 +154,14 @@ int veda_index_lists(const uint8_t* block_mask, int64_t n_heads,
  * with their own (row, head) strides. Lists: int32, cnt [H', n_q_tiles],
  * idx [H', n_q_tiles, list_ld]. lse: fp32 or NULL, element
  * lse[h * lse_stride_h + row * lse_stride_s]. head_dim: 128.
+ * front_tiles (0 .. n_q_tiles): query tiles [n_q_tiles - front_tiles,
+ * n_q_tiles) of every head are dispatched before all others. It changes no
+ * value, only the order: pass the number of tiles the mask makes dense
+ * (miowtion/veda/mask.py:288-317 keeps every key tile for the global rows,
+ * which come last in tile order), so that their long walks do not end the
+ * launch; 0 is the plain (head, tile) order. The same argument of
+ * veda_compensated_attention and veda_block_sparse_bwd (there it also
+ * orders the key tiles of the dK / dV kernel) means the same.
  */
 int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t q_stride_h,
                           const void* k, int64_t k_stride_s, int64_t k_stride_h,
@@ -165,7 +173,7 @@ int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t q_stride_h,
                           int64_t list_ld, const int32_t* valid_count,
                           float scale, void* out, int64_t o_stride_s,
                           int64_t o_stride_h, float* lse, int64_t lse_stride_h,
-                          int64_t lse_stride_s, void* stream);
+                          int64_t lse_stride_s, int64_t front_tiles, void* stream);
 
 /*
  * Dense attention of rows [0, used) among themselves on packed [S, H, D]
@@ -306,7 +314,7 @@ int veda_compensated_attention(const void* q, int64_t q_stride_s, int64_t q_stri
                                const void* vc, int64_t c_stride_s, int64_t c_stride_h,
                                const uint8_t* keep, const int32_t* valid_count, float scale,
                                void* out, int64_t o_stride_s, int64_t o_stride_h,
-                               void* stream);
+                               int64_t front_tiles, void* stream);
 
 /*
  * Block-sparse attention backward: the gradients of veda_block_sparse_fwd
@@ -347,7 +355,7 @@ int veda_block_sparse_bwd(const void* q, int64_t q_stride_s, int64_t q_stride_h,
                           int64_t dq_stride_s, int64_t dq_stride_h, void* dk,
                           int64_t dk_stride_s, int64_t dk_stride_h, void* dv,
                           int64_t dv_stride_s, int64_t dv_stride_h, void* workspace,
-                          int64_t workspace_bytes, void* stream);
+                          int64_t workspace_bytes, int64_t front_tiles, void* stream);
 
 /*
  * Predictor tile embedding, miowtion/veda/predictor.py:251-255:

@@ -30,7 +30,7 @@ SIGNATURES: dict[str, list] = {
     'veda_dense_block_mask': [_P, _P, _I, _I, _I, _P, _I, _I, _C, _P, _P],
     'veda_index_lists': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     'veda_block_sparse_fwd': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I,
-                              _P, _P, _P, _P, _I, _P, _F, _P, _I, _I, _P, _I, _I, _P],
+                              _P, _P, _P, _P, _I, _P, _F, _P, _I, _I, _P, _I, _I, _I, _P],
     'veda_dense_fwd': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _F, _P,
                        _I, _I, _P, _I, _I, _P],
     'veda_block_heat': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I,
@@ -44,10 +44,10 @@ SIGNATURES: dict[str, list] = {
     'veda_block_sparse_bwd': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _I,
                               _P, _I, _I, _P, _I, _I, _I, _I, _I, _I,
                               _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _F,
-                              _P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _P],
+                              _P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _I, _P],
     'veda_compensated_attention': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I,
                                    _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P, _F,
-                                   _P, _I, _I, _P],
+                                   _P, _I, _I, _I, _P],
     'veda_predictor_embed': [_P, _I, _I, _I, _P, _C, _P, _I, _P, _I, _C, _P, _P],
     'veda_predictor_logits': [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _C, _P, _P],
 }

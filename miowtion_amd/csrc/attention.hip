@@ -84,6 +84,7 @@ struct FwdParams {
   int64_t lk_h, lk_s;
   float* part;
   int64_t part_sh, part_st;
+  int64_t front;  // sparse walks: query tiles [n_q - front, n_q) of every head go first
 };
 
 // Key walks: the block lists (sparse forward), every row of a packed
@@ -838,9 +839,8 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 31, hi = lane >> 5;
-  const int64_t item = blockIdx.x;
-  const int64_t head = item / p.n_q_tiles;
-  const int64_t r = item % p.n_q_tiles;
+  int64_t head, r;
+  front_first(blockIdx.x, p.n_heads, p.n_q_tiles, p.front, head, r);
   const int64_t qrow = r * kTile + 32 * wave + li;
   const int nk = (int)p.n_k_tiles;
 
@@ -1110,9 +1110,12 @@ extern "C" int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t 
                                      const int32_t* part_idx, int64_t list_ld,
                                      const int32_t* valid_count, float scale, void* out,
                                      int64_t o_stride_s, int64_t o_stride_h, float* lse,
-                                     int64_t lse_stride_h, int64_t lse_stride_s, void* stream) {
+                                     int64_t lse_stride_h, int64_t lse_stride_s,
+                                     int64_t front_tiles, void* stream) {
   VEDA_REQUIRE(head_dim == kD, "block_sparse_fwd: head_dim must be 128, got %lld",
                (long long)head_dim);
+  VEDA_REQUIRE(front_tiles >= 0 && front_tiles <= n_q_tiles,
+               "block_sparse_fwd: front_tiles %lld outside [0, n_q_tiles]", (long long)front_tiles);
   VEDA_REQUIRE(n_heads >= 0 && n_q_tiles >= 0 && n_k_tiles >= 0, "block_sparse_fwd: negative size");
   VEDA_REQUIRE(list_ld >= n_k_tiles, "block_sparse_fwd: list_ld %lld < n_k_tiles %lld",
                (long long)list_ld, (long long)n_k_tiles);
@@ -1144,6 +1147,7 @@ extern "C" int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t 
   p.out = static_cast<uint16_t*>(out);
   p.os = o_stride_s; p.oh = o_stride_h;
   p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
+  p.front = front_tiles;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   sfwd_kernel<kSparse><<<(unsigned)items, kThreads2, 0, s>>>(p);
   return check_launch("veda_block_sparse_fwd");
@@ -1156,9 +1160,12 @@ extern "C" int veda_compensated_attention(
     const int32_t* full_idx, const int32_t* part_cnt, const int32_t* part_idx, int64_t list_ld,
     const void* kc, const void* vc, int64_t c_stride_s, int64_t c_stride_h, const uint8_t* keep,
     const int32_t* valid_count, float scale, void* out, int64_t o_stride_s, int64_t o_stride_h,
-    void* stream) {
+    int64_t front_tiles, void* stream) {
   VEDA_REQUIRE(head_dim == kD, "compensated_attention: head_dim must be 128, got %lld",
                (long long)head_dim);
+  VEDA_REQUIRE(front_tiles >= 0 && front_tiles <= n_q_tiles,
+               "compensated_attention: front_tiles %lld outside [0, n_q_tiles]",
+               (long long)front_tiles);
   VEDA_REQUIRE(n_heads >= 0 && n_q_tiles >= 0 && n_k_tiles >= 0,
                "compensated_attention: negative size");
   VEDA_REQUIRE(list_ld >= n_k_tiles, "compensated_attention: list_ld %lld < n_k_tiles %lld",
@@ -1196,6 +1203,7 @@ extern "C" int veda_compensated_attention(
   p.kc = static_cast<const uint16_t*>(kc);
   p.vc = static_cast<const uint16_t*>(vc);
   p.cs = c_stride_s; p.ch = c_stride_h;
+  p.front = front_tiles;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   sfwd_kernel<kSparseComp><<<(unsigned)items, kThreads2, 0, s>>>(p);
   return check_launch("veda_compensated_attention");

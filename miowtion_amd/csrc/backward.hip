@@ -86,6 +86,7 @@ struct BwdParams {
   uint16_t* dk;
   uint16_t* dv;
   int64_t dqs, dqh, dks, dkh, dvs, dvh;
+  int64_t front;  // the last `front` query tiles (dQ) and key tiles (dK, dV) go first
 };
 
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
@@ -243,8 +244,8 @@ __global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 31, hi = lane >> 5;
   const int qg = wave & 3, kh = wave >> 2;
-  const int64_t item = blockIdx.x;
-  const int64_t head = item / p.n_q_tiles, r = item % p.n_q_tiles;
+  int64_t head, r;
+  front_first(blockIdx.x, p.n_heads, p.n_q_tiles, p.front, head, r);
   const int64_t qrow = r * kTile + 32 * qg + li;
   const int nk = (int)p.n_k_tiles;
 
@@ -404,8 +405,8 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
   const int li = lane & 31, hi = lane >> 5;
   const int kg = wave & 3;
   const bool pwave = wave < 4;  // S, P, dV; else dP, dS, dK
-  const int64_t item = blockIdx.x;
-  const int64_t head = item / p.n_k_tiles, j = item % p.n_k_tiles;
+  int64_t head, j;
+  front_first(blockIdx.x, p.n_heads, p.n_k_tiles, p.front, head, j);
   const int vc = __builtin_amdgcn_readfirstlane(clamp_vc(p.valid_count[j]));
   const int64_t krow = j * kTile + 32 * kg + li;
   const int nq = (int)p.n_q_tiles;
@@ -589,7 +590,7 @@ extern "C" int veda_block_sparse_bwd(
     int64_t list_ld_t, const int32_t* valid_count, float scale, void* dq, int64_t dq_stride_s,
     int64_t dq_stride_h, void* dk, int64_t dk_stride_s, int64_t dk_stride_h, void* dv,
     int64_t dv_stride_s, int64_t dv_stride_h, void* workspace, int64_t workspace_bytes,
-    void* stream) {
+    int64_t front_tiles, void* stream) {
   VEDA_REQUIRE(head_dim == kD, "block_sparse_bwd: head_dim must be 128, got %lld",
                (long long)head_dim);
   VEDA_REQUIRE(n_heads >= 0 && n_q_tiles >= 0 && n_k_tiles >= 0, "block_sparse_bwd: negative size");
@@ -613,6 +614,9 @@ extern "C" int veda_block_sparse_bwd(
   VEDA_REQUIRE(q_stride_s < (1 << 24) && k_stride_s < (1 << 24) && v_stride_s < (1 << 24) &&
                    do_stride_s < (1 << 24),
                "block_sparse_bwd: row stride too large");
+  VEDA_REQUIRE(front_tiles >= 0 && front_tiles <= n_q_tiles && front_tiles <= n_k_tiles,
+               "block_sparse_bwd: front_tiles %lld outside [0, min(n_q_tiles, n_k_tiles)]",
+               (long long)front_tiles);
   const int64_t need = n_heads * 2 * n_q_tiles * kRecBytes;
   VEDA_REQUIRE(aligned16(workspace) && workspace_bytes >= need,
                "block_sparse_bwd: workspace needs %lld bytes (16-byte aligned), got %lld",
@@ -646,6 +650,7 @@ extern "C" int veda_block_sparse_bwd(
   p.dqs = dq_stride_s; p.dqh = dq_stride_h;
   p.dks = dk_stride_s; p.dkh = dk_stride_h;
   p.dvs = dv_stride_s; p.dvh = dv_stride_h;
+  p.front = front_tiles;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t q_items = n_heads * n_q_tiles, k_items = n_heads * n_k_tiles;
   if (q_items > 0) {

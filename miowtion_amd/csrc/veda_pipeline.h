@@ -81,6 +81,26 @@ __device__ __forceinline__ void dma16(const char* base, uint32_t voff, const lds
       : "memory", "m0");
 }
 
+// Workgroup order with the last `front` tiles of every head first: block b
+// < heads * front takes (head b / front, tile n - front + b % front), the
+// other blocks the remaining tiles head by head. Tiles that a mask makes
+// dense (global rows or columns) have the longest walks; dispatching them
+// first keeps them off the end of the launch. front = 0 is the plain
+// (head, tile) order.
+__device__ __forceinline__ void front_first(int64_t b, int64_t n_heads, int64_t n, int64_t front,
+                                            int64_t& head, int64_t& tile) {
+  const int64_t lead = n_heads * front;
+  if (b < lead) {
+    head = b / front;
+    tile = n - front + b % front;
+  } else {
+    const int64_t rest = n - front;
+    b -= lead;
+    head = b / rest;
+    tile = b % rest;
+  }
+}
+
 // vmcnt waits as s_waitcnt immediates (gfx9 encoding: vmcnt low bits [3:0],
 // expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
 #define VEDA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))

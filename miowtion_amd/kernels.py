@@ -124,6 +124,14 @@ def index_lists(block_mask: torch.Tensor, layout: tiling.TileLayout,
             torch.where(full_row[..., None], idx, empty_idx).contiguous())
 
 
+def _front_tiles(layout: tiling.TileLayout, rows: int) -> int:
+    """Tiles dispatched first: the ones a Veda mask makes dense (the global
+    rows keep every key tile and every row keeps the global columns,
+    mask.py:288-317; they come after the video tiles in tile order), when
+    all `rows` query tiles are present. Order only, no value changes."""
+    return layout.n_tiles - layout.n_video_tiles if rows == layout.n_tiles else 0
+
+
 class _BlockSparseAttention(torch.autograd.Function):
     """Block-sparse attention with gradients: the forward kernel, then the
     backward kernels on the forward and the transposed block lists
@@ -135,7 +143,8 @@ class _BlockSparseAttention(torch.autograd.Function):
     def forward(ctx, q, k, v, block_mask, layout):
         lists = index_lists(block_mask, layout)
         lists_t = index_lists(block_mask, layout, transpose=True)
-        out, lse = ops.block_sparse_fwd(q, k, v, *lists, layout.valid_count, True)
+        ctx.front = _front_tiles(layout, q.shape[0] // 128)
+        out, lse = ops.block_sparse_fwd(q, k, v, *lists, layout.valid_count, True, ctx.front)
         ctx.save_for_backward(q, k, v, out, lse, *lists, *lists_t, layout.valid_count)
         ctx.set_materialize_grads(False)
         return out, lse
@@ -148,7 +157,7 @@ class _BlockSparseAttention(torch.autograd.Function):
             dout = torch.zeros_like(out)
         dq, dk, dv = ops.block_sparse_bwd(
             q, k, v, out, dout.contiguous(), lse, None if dlse is None else dlse.contiguous(),
-            *lists, *lists_t, valid_count)
+            *lists, *lists_t, valid_count, ctx.front)
         return dq, dk, dv, None, None
 
 
@@ -186,7 +195,8 @@ def block_sparse_attention_lists(q, k, v, lists, layout: tiling.TileLayout,
     full_cnt, full_idx) lists (the BlockSparseTensorsTorch path of fa4.py)."""
     part_cnt, part_idx, full_cnt, full_idx = lists
     res = ops.block_sparse_fwd(q, k, v, part_cnt, part_idx, full_cnt, full_idx,
-                               layout.valid_count, return_lse)
+                               layout.valid_count, return_lse,
+                               _front_tiles(layout, q.shape[0] // 128))
     return (res[0], res[1]) if return_lse else res[0]
 
 
@@ -280,4 +290,5 @@ def compensated_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if lists is None:
         lists = index_lists(kept, layout)
     kc, vc = tile_summaries(k, v, layout)
-    return ops.compensated_attention(q, k, v, *lists, kc, vc, kept, layout.valid_count)
+    return ops.compensated_attention(q, k, v, *lists, kc, vc, kept, layout.valid_count,
+                                     _front_tiles(layout, q.shape[0] // 128))

@@ -222,8 +222,10 @@ def _(block_mask, kv_ok, full_tile):
 def block_sparse_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      part_cnt: torch.Tensor, part_idx: torch.Tensor, full_cnt: torch.Tensor,
                      full_idx: torch.Tensor, valid_count: torch.Tensor,
-                     return_lse: bool) -> list[torch.Tensor]:
-    """-> [out] or [out, lse [H', R*128]]; lists as returned by index_lists."""
+                     return_lse: bool, front_tiles: int = 0) -> list[torch.Tensor]:
+    """-> [out] or [out, lse [H', R*128]]; lists as returned by index_lists.
+    front_tiles: the last query tiles of every head to dispatch first (the
+    rows the mask makes dense); it changes the order only."""
     _require_gpu(q, k, v, part_cnt, part_idx, full_cnt, full_idx, valid_count)
     for name, t in (('q', q), ('k', k), ('v', v)):
         _check_rows(name, t)
@@ -250,12 +252,12 @@ def block_sparse_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                  r_tiles, n_k, full_cnt.data_ptr(), full_idx.data_ptr(), part_cnt.data_ptr(),
                  part_idx.data_ptr(), part_idx.shape[3], valid_count.data_ptr(),
                  1.0 / math.sqrt(d), out.data_ptr(), out.stride(0), out.stride(1), _p(lse),
-                 rq, 1, _stream(q))
+                 rq, 1, front_tiles, _stream(q))
     return [out, lse] if return_lse else [out]
 
 
 @block_sparse_fwd.register_fake
-def _(q, k, v, part_cnt, part_idx, full_cnt, full_idx, valid_count, return_lse):
+def _(q, k, v, part_cnt, part_idx, full_cnt, full_idx, valid_count, return_lse, front_tiles=0):
     out = torch.empty_like(q)
     if return_lse:
         return [out, q.new_empty(q.shape[1], q.shape[0], dtype=torch.float32)]
@@ -277,7 +279,7 @@ def block_sparse_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: tor
                      part_cnt: torch.Tensor, part_idx: torch.Tensor, full_cnt: torch.Tensor,
                      full_idx: torch.Tensor, part_cnt_t: torch.Tensor, part_idx_t: torch.Tensor,
                      full_cnt_t: torch.Tensor, full_idx_t: torch.Tensor,
-                     valid_count: torch.Tensor) -> list[torch.Tensor]:
+                     valid_count: torch.Tensor, front_tiles: int = 0) -> list[torch.Tensor]:
     """-> [dq, dk, dv] of block_sparse_fwd (fa4_sm8x/interface.py:2099
     _flash_attn_bwd with the Q-direction lists). lse: the forward's [H', R*128]
     fp32 LSE; dlse: its gradient or None; *_t: index_lists(transpose=True)."""
@@ -319,13 +321,13 @@ def block_sparse_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: tor
                  part_idx_t.data_ptr(), part_idx_t.shape[3], valid_count.data_ptr(),
                  1.0 / math.sqrt(d), dq.data_ptr(), dq.stride(0), dq.stride(1), dk.data_ptr(),
                  dk.stride(0), dk.stride(1), dv.data_ptr(), dv.stride(0), dv.stride(1),
-                 work.data_ptr(), work.numel() * 4, _stream(q))
+                 work.data_ptr(), work.numel() * 4, front_tiles, _stream(q))
     return [dq, dk, dv]
 
 
 @block_sparse_bwd.register_fake
 def _(q, k, v, out, dout, lse, dlse, part_cnt, part_idx, full_cnt, full_idx, part_cnt_t,
-      part_idx_t, full_cnt_t, full_idx_t, valid_count):
+      part_idx_t, full_cnt_t, full_idx_t, valid_count, front_tiles=0):
     return [torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)]
 
 
@@ -545,7 +547,8 @@ def _(o_kept, lse_kept, q, kc, vc, block_mask, valid_count):
 def compensated_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           part_cnt: torch.Tensor, part_idx: torch.Tensor, full_cnt: torch.Tensor,
                           full_idx: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor,
-                          block_mask: torch.Tensor, valid_count: torch.Tensor) -> torch.Tensor:
+                          block_mask: torch.Tensor, valid_count: torch.Tensor,
+                          front_tiles: int = 0) -> torch.Tensor:
     """Block-sparse attention over the listed (kept) blocks plus the
     zero-order term of every other non-empty key tile, in one pass
     (compensation_triton.attention, :228-258). Lists as index_lists returns
@@ -578,12 +581,13 @@ def compensated_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                  part_cnt.data_ptr(), part_idx.data_ptr(), part_idx.shape[3], kc.data_ptr(),
                  vc.data_ptr(), kc.stride(0), kc.stride(1), keep.data_ptr(),
                  valid_count.contiguous().data_ptr(), 1.0 / math.sqrt(d), out.data_ptr(),
-                 out.stride(0), out.stride(1), _stream(q))
+                 out.stride(0), out.stride(1), front_tiles, _stream(q))
     return out
 
 
 @compensated_attention.register_fake
-def _(q, k, v, part_cnt, part_idx, full_cnt, full_idx, kc, vc, block_mask, valid_count):
+def _(q, k, v, part_cnt, part_idx, full_cnt, full_idx, kc, vc, block_mask, valid_count,
+      front_tiles=0):
     return torch.empty_like(q)
 
 

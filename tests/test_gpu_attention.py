@@ -154,3 +154,23 @@ def test_sampled_query_tiles_at_config2_size():
     real = olay.slot_valid.view(-1, 128)[rows].reshape(-1).bool()
     _close(got, ref, real)
     _close(got_lse.T, ref_lse.T, real)
+
+
+def test_front_tiles_change_the_order_only():
+    """Dispatching the global query tiles (dense rows, last in tile order)
+    first gives the same bits as the plain order, forward and backward."""
+    from miowtion_amd import ops
+    lay, olay, qt, kt, vt, mask = _case(helpers.small_layout())
+    front = lay.n_tiles - lay.n_video_tiles
+    assert front > 0
+    q, k, v, m = qt.cuda(), kt.cuda(), vt.cuda(), mask.cuda()
+    lists = kernels.index_lists(m, lay)
+    a = ops.block_sparse_fwd(q, k, v, *lists, lay.valid_count, True, 0)
+    b = ops.block_sparse_fwd(q, k, v, *lists, lay.valid_count, True, front)
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+    lists_t = kernels.index_lists(m, lay, transpose=True)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16).cuda()
+    ga = ops.block_sparse_bwd(q, k, v, a[0], dout, a[1], None, *lists, *lists_t, lay.valid_count, 0)
+    gb = ops.block_sparse_bwd(q, k, v, a[0], dout, a[1], None, *lists, *lists_t, lay.valid_count,
+                              front)
+    assert all(torch.equal(x, y) for x, y in zip(ga, gb))

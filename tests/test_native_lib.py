@@ -50,7 +50,10 @@ def test_host_side_argument_checks():
                      None, None, 0, 0, 0, None)
     with pytest.raises(ValueError, match='head_dim'):
         _native.call('veda_block_sparse_fwd', None, 0, 0, None, 0, 0, None, 0, 0, 1, 64, 1, 1,
-                     None, None, None, None, 1, None, 1.0, None, 0, 0, None, 0, 0, None)
+                     None, None, None, None, 1, None, 1.0, None, 0, 0, None, 0, 0, 0, None)
+    with pytest.raises(ValueError, match='front_tiles'):
+        _native.call('veda_block_sparse_fwd', None, 0, 0, None, 0, 0, None, 0, 0, 1, 128, 1, 1,
+                     None, None, None, None, 1, None, 1.0, None, 0, 0, None, 0, 0, 2, None)
     with pytest.raises(ValueError, match='reduce'):
         _native.call('veda_block_heat', None, 0, 0, None, 0, 0, None, 0, 0, None, None, 1, 1,
                      1, 128, 3, 1.0, None, None)
@@ -69,11 +72,11 @@ def test_host_side_argument_checks():
     with pytest.raises(ValueError, match='head_dim'):
         _native.call('veda_block_sparse_bwd', *([None, 0, 0] * 7), 1, 64, 1, 1, None, None,
                      None, None, 1, None, None, None, None, 1, None, 1.0, *([None, 0, 0] * 3),
-                     None, 0, None)
+                     None, 0, 0, None)
     with pytest.raises(ValueError, match='workspace'):
         _native.call('veda_block_sparse_bwd', *([16, 0, 0] * 5), 16, 0, 0, None, 0, 0, 1, 128,
                      1, 1, None, None, None, None, 1, None, None, None, None, 1, None, 1.0,
-                     *([16, 0, 0] * 3), 16, 1024, None)
+                     *([16, 0, 0] * 3), 16, 1024, 0, None)
     with pytest.raises(ValueError, match='reduce'):
         _native.call('veda_heat_combine', None, None, 0, 0, None, None, 1, 1, 1, 5, None, None)
     assert isinstance(lib.veda_last_error(), bytes)
