@@ -1,8 +1,10 @@
 // Flash-attention forwards for gfx950 (head_dim 128, bf16 in, fp32
 // accumulate). Two kernels share the step, fragment and load code below:
-//   hfwd_kernel  the dense forward and the teacher's all-tiles pass;
-//   sfwd_kernel  the block-sparse forward and the zero-order compensation
-//                (two 4-wave workgroups per CU, described at its section).
+//   hfwd_kernel  the teacher's pass over all key tiles in tile order (block
+//                heat statistics, optionally the dense output);
+//   sfwd_kernel  the block-sparse forward, the zero-order compensation and
+//                the dense forward of packed rows (two 4-wave workgroups
+//                per CU, described at its section).
 //
 // hfwd_kernel: workgroup = one (head, 128-row query tile), 8 waves, 1 per CU:
 //   wave w: query group qg = w & 3 (32 query rows), key half kh = w >> 2;
@@ -57,9 +59,8 @@ struct FwdParams {
   const int32_t* part_idx;
   int64_t list_ld;
   const int32_t* valid_count;
-  int64_t used;      // dense mode: real rows; sparse mode: unused
-  int64_t kv_rows;   // rows of k / v that may be read (>= 1 when any block runs)
-  int64_t q_rows;    // rows of q / out / lse that exist
+  int64_t used;      // dense rows: real rows
+  int64_t q_rows;    // dense rows: rows of q / out / lse that exist
   float scale_log2;  // softmax scale * log2(e)
   uint16_t* out;
   int64_t os, oh;
@@ -87,10 +88,6 @@ struct FwdParams {
   int64_t front;  // sparse walks: query tiles [n_q - front, n_q) of every head go first
 };
 
-// Key walks: the block lists (sparse forward), every row of a packed
-// sequence (dense forward), or every key tile of a tile layout in order,
-// its padding rows masked (the teacher's dense pass in tile order).
-enum Walk { kLists = 0, kDense = 1, kAllTiles = 2 };
 // Block statistic collected for the teacher heat: none, log-sum-exp, max.
 enum Heat { kNoHeat = 0, kHeatSum = 1, kHeatMax = 2 };
 constexpr int32_t kTileEnd = 1 << 30;  // step-list flag: last step of its key tile
@@ -158,11 +155,9 @@ __device__ __forceinline__ HDma hdma_offsets(int64_t ks, int64_t vs, int wave, i
 }
 
 
-// Issues the loads of the step at key row row0 (64 rows, the first vch >= 1
-// of them valid) into `slot`. CLAMP (the dense path's last tile, whose rows past the
-// valid count may lie past the end of k / v): every lane reads a row below
-// vch instead. Without PV only K is loaded.
-template <bool CLAMP, bool PV>
+// Issues the loads of the step at key row row0 (64 rows, the first vch of
+// them valid) into `slot`. Without PV only K is loaded.
+template <bool PV>
 __device__ __forceinline__ void issue_step(const uint16_t* kbase, const uint16_t* vbase,
                                            const FwdParams& p, const HDma& d, int64_t row0,
                                            int vch, int wave, int lane, lds_u8* slot) {
@@ -172,18 +167,8 @@ __device__ __forceinline__ void issue_step(const uint16_t* kbase, const uint16_t
   for (int u = 0; u < 2; ++u) {
     const int seg = 2 * wave + u;
     const bool live = 4 * seg < vch;
-    uint32_t ko, vo;
-    if (CLAMP) {
-      const int lr = lane >> 4, pc = lane & 15, row = 4 * seg + lr;
-      const int src = min(live ? row : lr, vch - 1);
-      ko = (uint32_t)((src * p.ks + ((pc ^ (row & 15)) << 3)) * 2);
-      vo = (uint32_t)((src * p.vs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
-    } else {
-      ko = live ? d.k[u] : d.k_skip[u];
-      vo = live ? d.v[u] : d.v_skip[u];
-    }
-    dma16(kb, ko, slot + seg * 1024);
-    if (PV) dma16(vb, vo, slot + kHalfBytes + seg * 1024);
+    dma16(kb, live ? d.k[u] : d.k_skip[u], slot + seg * 1024);
+    if (PV) dma16(vb, live ? d.v[u] : d.v_skip[u], slot + kHalfBytes + seg * 1024);
   }
 }
 
@@ -286,22 +271,22 @@ __device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float 
 }
 
 
-template <int WALK, int HEAT, bool PV>
+// The teacher's pass: every key tile of a tile layout in order, its padding
+// rows masked, with the block statistic of the heat and, with PV, the
+// dense output.
+template <int HEAT, bool PV>
 __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
-  constexpr bool DENSE = WALK == kDense;
-  constexpr bool TILES = WALK == kAllTiles;
-  // Without PV a slot holds K only, and the all-tiles walk keeps its steps
-  // as 16-bit (tile, half) entries plus a byte per tile of valid counts:
-  // the statistics-only pass then needs 75 KB of LDS, so two workgroups
-  // share a CU and hide each other's latencies.
+  // Without PV a slot holds K only, and the steps are 16-bit (tile, half)
+  // entries plus a byte per tile of valid counts: the statistics-only pass
+  // then needs 75 KB of LDS, so two workgroups share a CU and hide each
+  // other's latencies.
   constexpr int kSlot = PV ? kSlotBytes : kHalfBytes;
   __shared__ __attribute__((aligned(1024))) uint8_t slot0[kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t slot1[kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t slot2[kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t slot3[kSlot];
-  __shared__ int32_t step_list[TILES ? 1 : 2 * kMaxBlocks];
-  __shared__ uint16_t tile_steps[TILES ? 2 * kMaxBlocks : 1];  // (key tile << 1) | half
-  __shared__ uint8_t tile_valid[TILES ? kMaxBlocks : 1];
+  __shared__ uint16_t tile_steps[2 * kMaxBlocks];  // (key tile << 1) | half
+  __shared__ uint8_t tile_valid[kMaxBlocks];
   __shared__ int32_t step_total;
   __shared__ float lbuf[2][4][32];  // heat: kh = 1 hands its key-tile partials to kh = 0
   lds_u8* sl0 = (lds_u8*)slot0;
@@ -316,32 +301,19 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   const int64_t head = item / p.n_q_tiles;
   const int64_t r = item % p.n_q_tiles;
   const int64_t qrow = r * kTile + 32 * qg + li;  // row of out / lse / part
-  // row of q (the all-tiles walk reads query tile q_tiles[r])
-  const int64_t qtile = TILES && p.q_tiles != nullptr ? p.q_tiles[r] : r;
-  const bool qtile_ok = !TILES || (qtile >= 0 && qtile < p.q_tiles_held);
-  const int64_t qsrc = TILES ? (qtile_ok ? qtile : 0) * kTile + 32 * qg + li : qrow;
+  // row of q: item r reads query tile q_tiles[r]
+  const int64_t qtile = p.q_tiles != nullptr ? p.q_tiles[r] : r;
+  const bool qtile_ok = qtile >= 0 && qtile < p.q_tiles_held;
+  const int64_t qsrc = (qtile_ok ? qtile : 0) * kTile + 32 * qg + li;
 
   // The ring needs no clearing: every step's loads write all 64 rows of
   // its slot (segments past the valid count re-read real rows), so an MFMA
   // only ever reads rows its own step wrote.
 
-  // Step list: one word per step, (first key row << 7) | valid keys of the
-  // step (0..64). Blocks in walk order (full list first): a full key tile
-  // is two steps; a partial tile is one step for its first half, plus one
-  // for its second half when more than 64 keys are valid -- those second
-  // halves go after all first halves, in walk order (ranked by a ballot,
-  // so the list, and with it the summation order, is deterministic). An
-  // entry outside [0, n_k_tiles) keeps no key (steps with 0 valid keys,
-  // loading tile 0). The dense path needs no list: step u is rows
-  // 64 u .. 64 u + 63.
-  int n_steps;
-  if (DENSE) {
-    const int64_t nsteps = (p.used + kHalf - 1) / kHalf;
-    n_steps = (int)nsteps;
-  } else if (TILES) {
-    // Every key tile in order, its steps consecutive: the first half, then
-    // the second half when more than 64 keys are valid; the tile's last step
-    // carries kTileEnd. An empty tile is one step with no valid key.
+  // Steps: every key tile in order, its steps consecutive: the first half,
+  // then the second half when more than 64 keys are valid; the tile's last
+  // step carries kTileEnd. An empty tile is one step with no valid key.
+  {
     if (wave == 0) {
       const int nk = (int)p.n_k_tiles;
       int base = 0;
@@ -362,50 +334,12 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
       }
       if (lane == 0) step_total = base;
     }
-  } else {
-    const int64_t li_ = head * p.n_q_tiles + r;
-    const int ld = (int)p.list_ld;
-    const int nf = min(max(p.full_cnt[li_], 0), min(ld, kMaxBlocks));
-    const int np = min(max(p.part_cnt[li_], 0), min(ld, kMaxBlocks - nf));
-    const int32_t* fl = p.full_idx + li_ * p.list_ld;
-    const int32_t* pl = p.part_idx + li_ * p.list_ld;
-    for (int i = tid; i < nf; i += kThreads) {
-      const int32_t j = fl[i];
-      const bool ok = j >= 0 && j < p.n_k_tiles;
-      const int32_t row0 = ok ? j * kTile : 0;
-      step_list[2 * i] = (row0 << 7) | (ok ? kHalf : 0);
-      step_list[2 * i + 1] = ((row0 + kHalf) << 7) | (ok ? kHalf : 0);
-    }
-    if (wave == 0) {
-      int h1 = 0;
-      for (int i0 = 0; i0 < np; i0 += 64) {
-        const int i = i0 + lane;
-        int32_t row0 = 0;
-        int vc = 0;
-        if (i < np) {
-          const int32_t j = pl[i];
-          if (j >= 0 && j < p.n_k_tiles) {
-            row0 = j * kTile;
-            vc = p.valid_count[j];
-          }
-          step_list[2 * nf + i] = (row0 << 7) | min(vc, kHalf);
-        }
-        const bool two = i < np && vc > kHalf;
-        const uint64_t bal = __ballot(two);
-        const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
-        if (two) step_list[2 * nf + np + h1 + rank] = ((row0 + kHalf) << 7) | (vc - kHalf);
-        h1 += __builtin_popcountll(bal);
-      }
-      if (lane == 0) step_total = 2 * nf + np + h1;
-    }
   }
 
   WaveState w;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
-    const bool q_ok = DENSE ? (qrow < p.used) : qtile_ok;
-    u32x4 v = q_ok ? ld16(p.q + qsrc * p.qs + head * p.qh + 16 * s + 8 * hi) : u32x4{0, 0, 0, 0};
+    u32x4 v = qtile_ok ? ld16(p.q + qsrc * p.qs + head * p.qh + 16 * s + 8 * hi) : u32x4{0, 0, 0, 0};
     w.qf[s] = as_bf16x8(v);
   }
 #pragma unroll
@@ -418,46 +352,30 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   w.l_run = 0.f;
   w.mu = 0.f;
   w.blk = HEAT == kHeatMax ? -INFINITY : 0.f;
-  __syncthreads();  // step list, step count and zeroed ring ready
-  if (!DENSE) n_steps = __builtin_amdgcn_readfirstlane(step_total);
+  __syncthreads();  // step list and step count ready
+  const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
 
   // Step word of step u: (first key row << 7) | valid keys | kTileEnd.
   auto step_word = [&](int u) -> int32_t {
-    if (TILES) {
-      const int e = __builtin_amdgcn_readfirstlane(tile_steps[u]);
-      const int j = e >> 1, half = e & 1;
-      const int vc = __builtin_amdgcn_readfirstlane(tile_valid[j]);
-      const int vch = half ? vc - kHalf : min(vc, kHalf);
-      return ((j * kTile + half * kHalf) << 7) | vch | ((half || vc <= kHalf) ? kTileEnd : 0);
-    }
-    return __builtin_amdgcn_readfirstlane(step_list[u]);
+    const int e = __builtin_amdgcn_readfirstlane(tile_steps[u]);
+    const int j = e >> 1, half = e & 1;
+    const int vc = __builtin_amdgcn_readfirstlane(tile_valid[j]);
+    const int vch = half ? vc - kHalf : min(vc, kHalf);
+    return ((j * kTile + half * kHalf) << 7) | vch | ((half || vc <= kHalf) ? kTileEnd : 0);
   };
   // (first key row, valid keys) of step u
-  auto step_row = [&](int u) -> int64_t {
-    return DENSE ? (int64_t)u * kHalf
-                 : (int64_t)((step_word(u) >> 7) & 0x7FFFFF);
-  };
-  auto step_vch = [&](int u) -> int {
-    if (DENSE) {
-      const int64_t rem = p.used - (int64_t)u * kHalf;
-      return rem < kHalf ? (int)rem : kHalf;
-    }
-    return step_word(u) & 127;
-  };
+  auto step_row = [&](int u) -> int64_t { return (int64_t)((step_word(u) >> 7) & 0x7FFFFF); };
+  auto step_vch = [&](int u) -> int { return step_word(u) & 127; };
   const uint16_t* kbase = p.k + head * p.kh;
   const uint16_t* vbase = p.v + head * p.vh;
   const float c = p.scale_log2;
   const HDma dma = hdma_offsets(p.ks, p.vs, wave, lane);
   const HFrag frag = hfrag_offsets(kh, lane);
 
+  // a step with no valid key (an empty tile) loads the tile's first rows,
+  // which exist; its keys are all masked
   auto load_step = [&](int u, lds_u8* slot) {
-    const int vch = step_vch(u);
-    // a step with no valid key (an empty or out-of-range tile) loads the
-    // tile's first rows, which exist; its keys are all masked
-    if (DENSE && vch < kHalf)
-      issue_step<true, PV>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
-    else
-      issue_step<false, PV>(kbase, vbase, p, dma, step_row(u), vch, wave, lane, slot);
+    issue_step<PV>(kbase, vbase, p, dma, step_row(u), step_vch(u), wave, lane, slot);
   };
   // Prologue: steps 0, 1, 2 into slots 0, 1, 2.
   if (n_steps > 0) load_step(0, sl0);
@@ -573,9 +491,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   const float a0 = __builtin_amdgcn_exp2f(w.m_run - mu);
   const float a1 = __builtin_amdgcn_exp2f(m1 - mu);
   const float l = w.l_run * a0 + l1 * a1;
-  const bool row_real = DENSE ? (qrow < p.used) : true;
-  const float inv = (l > 0.f && row_real) ? 1.f / l : 0.f;
-  if (qrow >= p.q_rows) return;  // dense mode: rows past seq_len do not exist
+  const float inv = l > 0.f ? 1.f / l : 0.f;
   uint16_t* orow = p.out + qrow * p.os + head * p.oh;
 #pragma unroll
   for (int dt = 0; dt < (PV ? 4 : 0); ++dt)
@@ -594,9 +510,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
       *reinterpret_cast<u32x2*>(orow + d) = u32x2{w0, w1};
     }
   if (p.lse != nullptr && hi == 0) {
-    float lse;
-    if (!row_real) lse = 0.f;
-    else lse = l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
+    const float lse = l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
     p.lse[head * p.lse_sh + qrow * p.lse_ss] = lse;
   }
 }
@@ -823,13 +737,17 @@ __device__ __forceinline__ void sstep_virtual(const lds_u8* slot, const HFrag& f
 // 1 + den. kSparseComp is compensated attention in one pass: the list steps,
 // then the virtual-key steps inside the same online softmax (a row that kept
 // nothing first gets the reference's unit mass at reference 0, with value 0,
-// so it ends as num / (1 + den) as well).
-enum SparseMode { kSparse = 0, kVirtualOnly = 1, kSparseComp = 2 };
+// so it ends as num / (1 + den) as well). kDenseRows is the dense forward
+// of packed rows: step u is key rows 64 u .. of the `used` real rows (the
+// last step clamped to them), and query rows at or past `used` get out 0
+// and lse 0.
+enum SparseMode { kSparse = 0, kVirtualOnly = 1, kSparseComp = 2, kDenseRows = 3 };
 
 template <int MODE>
 __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
-  constexpr bool LISTS = MODE != kVirtualOnly;  // walks the block lists
-  constexpr bool VKEYS = MODE != kSparse;       // walks the virtual keys
+  constexpr bool DENSE = MODE == kDenseRows;
+  constexpr bool LISTS = MODE == kSparse || MODE == kSparseComp;  // walks the block lists
+  constexpr bool VKEYS = MODE == kVirtualOnly || MODE == kSparseComp;  // walks the virtual keys
   __shared__ __attribute__((aligned(1024))) uint8_t ring[2][kSlotBytes];
   __shared__ uint16_t steps[LISTS ? 2 * kMaxBlocks : 1];
   __shared__ uint8_t tvc[LISTS ? kMaxBlocks : 1];
@@ -855,7 +773,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     }
   }
   if (!LISTS) {
-    if (tid == 0) step_total = 0;
+    if (tid == 0) step_total = DENSE ? (int)((p.used + kHalf - 1) / kHalf) : 0;
   } else {
     // Step list: full-list tiles as two unmasked halves, then the first
     // halves of the partial-list tiles, then their second halves (those with
@@ -900,7 +818,9 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   WaveState w;
 #pragma unroll
   for (int s = 0; s < 8; ++s)
-    w.qf[s] = as_bf16x8(ld16(p.q + qrow * p.qs + head * p.qh + 16 * s + 8 * hi));
+    w.qf[s] = (!DENSE || qrow < p.used)
+                  ? as_bf16x8(ld16(p.q + qrow * p.qs + head * p.qh + 16 * s + 8 * hi))
+                  : as_bf16x8(u32x4{0, 0, 0, 0});
 #pragma unroll
   for (int s = 0; s < 8; ++s) asm volatile("" : : "v"(w.qf[s]));
 #pragma unroll
@@ -926,6 +846,11 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       const int v = u - n_lsteps;
       row0 = (int64_t)v * kHalf;
       vch = min(nk - v * kHalf, kHalf);
+      return;
+    }
+    if (DENSE) {
+      row0 = (int64_t)u * kHalf;
+      vch = (int)min(p.used - row0, (int64_t)kHalf);
       return;
     }
     const int e = __builtin_amdgcn_readfirstlane(steps[u]);
@@ -975,6 +900,20 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     }
     const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
     const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
+    if (DENSE && vch < kHalf) {
+      // the last dense step: rows past `used` may not exist, so every lane
+      // reads a row below vch (masked keys)
+      const int lr = lane >> 4, pc = lane & 15;
+#pragma unroll
+      for (int u4 = 0; u4 < 4; ++u4) {
+        const int seg = 4 * wave + u4, row = 4 * seg + lr, src = min(row, vch - 1);
+        const uint32_t ko = (uint32_t)((src * p.ks + ((pc ^ (row & 15)) << 3)) * 2);
+        const uint32_t vo = (uint32_t)((src * p.vs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
+        dma16(kb, ko, slot + seg * 1024);
+        dma16(vb, vo, slot + kHalfBytes + seg * 1024);
+      }
+      return;
+    }
 #pragma unroll
     for (int u4 = 0; u4 < 4; ++u4) {
       const int seg = 4 * wave + u4;
@@ -1064,7 +1003,9 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   const float l = half_swap_sum(w.l_run);
   // compensation: the kept output is num / den over the kept keys with
   // den = 1 at the reference, hence out = (o_kept + num) / (1 + den)
-  const float inv = MODE == kVirtualOnly ? 1.f / (1.f + l) : l > 0.f ? 1.f / l : 0.f;
+  const bool row_real = !DENSE || qrow < p.used;
+  const float inv = MODE == kVirtualOnly ? 1.f / (1.f + l) : (l > 0.f && row_real) ? 1.f / l : 0.f;
+  if (DENSE && qrow >= p.q_rows) return;  // rows past seq_len do not exist
   uint16_t* orow = p.out + qrow * p.os + head * p.oh;
   const uint16_t* krow = MODE == kVirtualOnly ? p.o_kept + qrow * p.oks + head * p.okh : nullptr;
 #pragma unroll
@@ -1089,9 +1030,9 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       uint32_t w0 = pack_bf16x2(v4[0], v4[1]), w1 = pack_bf16x2(v4[2], v4[3]);
       *reinterpret_cast<u32x2*>(orow + d) = u32x2{w0, w1};
     }
-  if (MODE == kSparse && p.lse != nullptr && hi == 0)
+  if ((MODE == kSparse || DENSE) && p.lse != nullptr && hi == 0)
     p.lse[head * p.lse_sh + qrow * p.lse_ss] =
-        l > 0.f ? (w.m_run + __log2f(l)) * kLn2 : -INFINITY;
+        !row_real ? 0.f : l > 0.f ? (w.m_run + __log2f(l)) * kLn2 : -INFINITY;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1141,7 +1082,6 @@ extern "C" int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t 
   p.list_ld = list_ld;
   p.valid_count = valid_count;
   p.used = 0;
-  p.kv_rows = n_k_tiles * kTile;
   p.q_rows = n_q_tiles * kTile;
   p.scale_log2 = (float)((double)scale * 1.4426950408889634);
   p.out = static_cast<uint16_t*>(out);
@@ -1194,7 +1134,6 @@ extern "C" int veda_compensated_attention(
   p.part_cnt = part_cnt; p.part_idx = part_idx;
   p.list_ld = list_ld;
   p.valid_count = valid_count;
-  p.kv_rows = n_k_tiles * kTile;
   p.q_rows = n_q_tiles * kTile;
   p.scale_log2 = (float)((double)scale * 1.4426950408889634);
   p.out = static_cast<uint16_t*>(out);
@@ -1236,14 +1175,13 @@ extern "C" int veda_dense_fwd(const void* q, int64_t q_stride_s, int64_t q_strid
   p.n_heads = n_heads; p.n_q_tiles = n_q_tiles;
   p.n_k_tiles = (used + kTile - 1) / kTile;
   p.used = used;
-  p.kv_rows = used;
   p.q_rows = seq_len;
   p.scale_log2 = (float)((double)scale * 1.4426950408889634);
   p.out = static_cast<uint16_t*>(out);
   p.os = o_stride_s; p.oh = o_stride_h;
   p.lse = lse; p.lse_sh = lse_stride_h; p.lse_ss = lse_stride_s;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hfwd_kernel<kDense, kNoHeat, true><<<(unsigned)items, kThreads, 0, s>>>(p);
+  sfwd_kernel<kDenseRows><<<(unsigned)items, kThreads2, 0, s>>>(p);
   return check_launch("veda_dense_fwd");
 }
 
@@ -1301,11 +1239,11 @@ extern "C" int veda_dense_heat_fwd(const void* q, int64_t q_stride_s, int64_t q_
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const unsigned g = (unsigned)items;
   if (out != nullptr) {
-    if (reduce) hfwd_kernel<kAllTiles, kHeatMax, true><<<g, kThreads, 0, s>>>(p);
-    else hfwd_kernel<kAllTiles, kHeatSum, true><<<g, kThreads, 0, s>>>(p);
+    if (reduce) hfwd_kernel<kHeatMax, true><<<g, kThreads, 0, s>>>(p);
+    else hfwd_kernel<kHeatSum, true><<<g, kThreads, 0, s>>>(p);
   } else {
-    if (reduce) hfwd_kernel<kAllTiles, kHeatMax, false><<<g, kThreads, 0, s>>>(p);
-    else hfwd_kernel<kAllTiles, kHeatSum, false><<<g, kThreads, 0, s>>>(p);
+    if (reduce) hfwd_kernel<kHeatMax, false><<<g, kThreads, 0, s>>>(p);
+    else hfwd_kernel<kHeatSum, false><<<g, kThreads, 0, s>>>(p);
   }
   return check_launch("veda_dense_heat_fwd");
 }
