@@ -174,3 +174,37 @@ def test_front_tiles_change_the_order_only():
     gb = ops.block_sparse_bwd(q, k, v, a[0], dout, a[1], None, *lists, *lists_t, lay.valid_count,
                               front)
     assert all(torch.equal(x, y) for x, y in zip(ga, gb))
+
+
+def test_largest_tile_count():
+    """2048 tiles a side (FA4's cap on blocks per side, fa4_sm8x/block_sparsity.py:58-79;
+    the kernels' list and step tables are sized to it), partial tiles
+    included: sampled query tiles of the forward against the oracle; a
+    2049th tile is refused."""
+    spec = ([(0, (32, 62, 120))], 32 * 62 * 120, 32 * 62 * 120, '1x8x16')
+    lay = helpers.product_layout(*spec, device='cuda')
+    olay = helpers.oracle_layout(*spec)
+    assert lay.n_tiles == 2048 and int((olay.valid_count < 128).sum()) > 0
+    q, k, v = helpers.qkv(lay.seq_len, 1, 128, seed=3)
+    qt, kt, vt = (ot.gather_tiles(t, olay, None) for t in (q, k, v))
+    g = torch.Generator().manual_seed(4)
+    mask = torch.rand(1, 2048, 2048, generator=g) < 0.05
+    mask |= torch.eye(2048, dtype=torch.bool)[None]
+    mask[0, 7] = olay.kv_ok          # one dense row: the longest list (2048 tiles)
+    out, lse = kernels.block_sparse_attention(qt.cuda(), kt.cuda(), vt.cuda(), mask.cuda(), lay,
+                                              return_lse=True)
+    tiles = torch.tensor([0, 7, 1023, 2047])
+    rows = (tiles[:, None] * 128 + torch.arange(128)[None, :]).reshape(-1)
+    ref, ref_lse = oa.block_sparse_attention(qt[rows], kt, vt, mask[:, tiles], olay.valid_count,
+                                             return_lse=True)
+    real = olay.slot_valid.bool()[rows]
+    _close(out.cpu()[rows], ref, real)
+    _close(lse.cpu()[:, rows].T, ref_lse.T, real)
+    # a 2049th key tile is refused before anything is launched
+    from miowtion_amd import ops
+    kv = torch.zeros(2049 * 128, 1, 128, dtype=torch.bfloat16, device='cuda')
+    cnt = torch.zeros(1, 1, 1, dtype=torch.int32, device='cuda')
+    idx = torch.zeros(1, 1, 1, 2049, dtype=torch.int32, device='cuda')
+    with pytest.raises(ValueError, match='n_k_tiles'):
+        ops.block_sparse_fwd(qt[:128].cuda(), kv, kv, cnt, idx, cnt, idx,
+                             torch.full((2049,), 128, dtype=torch.int32, device='cuda'), False)

@@ -173,3 +173,27 @@ def test_config2_two_heads():
                                                    olay.valid_count, grad_out.cpu().float())
     for name, a, w in zip('qkv', got, want):
         _bar(a, w, name)
+
+
+def test_largest_tile_count():
+    """2048 tiles a side, one head, a dense row and a dense column (the
+    longest forward and transposed lists): every gradient row against the
+    per-tile oracle."""
+    spec = ([(0, (32, 62, 120))], 32 * 62 * 120, 32 * 62 * 120, '1x8x16')
+    lay = helpers.product_layout(*spec, device='cuda')
+    olay = helpers.oracle_layout(*spec)
+    assert lay.n_tiles == 2048
+    q, k, v = helpers.qkv(lay.seq_len, 1, 128, seed=8)
+    qt, kt, vt = (kernels.gather_tiles(t.cuda(), lay, None) for t in (q, k, v))
+    g = torch.Generator().manual_seed(6)
+    mask = torch.rand(1, 2048, 2048, generator=g) < 0.03
+    mask |= torch.eye(2048, dtype=torch.bool)[None]
+    mask[0, 5] = True
+    mask[0, :, 9] = True
+    mask &= olay.kv_ok[None, None, :]
+    grad_out = torch.randn(qt.shape, generator=g).to(torch.bfloat16)
+    got = _gpu_grads(qt, kt, vt, mask.cuda(), lay, grad_out.cuda())
+    want = oa.block_sparse_attention_grads_by_tile(qt.cpu(), kt.cpu(), vt.cpu(), mask,
+                                                   olay.valid_count, grad_out.float())
+    for name, a, w in zip('qkv', got, want):
+        _bar(a, w, name)
