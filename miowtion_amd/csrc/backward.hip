@@ -45,7 +45,7 @@ constexpr int kD = 128;
 constexpr int kMaxTiles = 2048;                  // tiles per list row (FA4's cap)
 constexpr int kRecFloats = 256;                  // stats record: 64 lse2, 64 D, 128 zero
 constexpr int kRecBytes = kRecFloats * 4;
-constexpr int kDqThreads = 512;
+constexpr int kDqThreads = 256;
 constexpr int kDkvThreads = 512;
 constexpr int kSlot = 2 * kHalfBytes;            // K + V (dq) or Q + dO (dkv) of a step
 constexpr float kLog2e = 1.4426950408889634f;
@@ -228,14 +228,15 @@ __global__ void __launch_bounds__(256) bwd_stats_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ. Workgroup = (head, query tile), 8 waves: wave w owns query rows
-// 32 (w % 4) .. + 31 (one per lane, as B = Q^T and dO^T fragments in
-// registers) and keys 32 (w / 4) .. + 31 of every 64-key step; the two key
-// halves keep separate dQ^T accumulators, summed through LDS at the end.
-// Per step and wave: S^T = K Q^T and dP^T = V dO^T (8 MFMAs each, A = K / V
-// rows from LDS), dS^T, then dQ^T += K^T dS^T (8 MFMAs, A = transposed K reads).
+// dQ. Workgroup = (head, query tile), 4 waves, two workgroups per CU (74 KB
+// of LDS each; their waves are not tied by a barrier, so the two waves of a
+// SIMD fill each other's stalls). Wave w owns query rows 32 w .. + 31 (one
+// per lane, as B = Q^T and dO^T fragments in registers) and both 32-key
+// halves of every 64-key step. Per half: S^T = K Q^T and dP^T = V dO^T (8
+// MFMAs each, A = K / V rows from LDS), dS^T, then dQ^T += K^T dS^T (8
+// MFMAs, A = transposed K reads).
 
-__global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
+__global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[2][kSlot];
   __shared__ uint16_t steps[2 * kMaxTiles];
   __shared__ uint8_t tvc[kMaxTiles];
@@ -243,10 +244,9 @@ __global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 31, hi = lane >> 5;
-  const int qg = wave & 3, kh = wave >> 2;
   int64_t head, r;
   front_first(blockIdx.x, p.n_heads, p.n_q_tiles, p.front, head, r);
-  const int64_t qrow = r * kTile + 32 * qg + li;
+  const int64_t qrow = r * kTile + 32 * wave + li;
   const int nk = (int)p.n_k_tiles;
 
   for (int j = tid; j < nk; j += kDqThreads) tvc[j] = (uint8_t)clamp_vc(p.valid_count[j]);
@@ -269,9 +269,9 @@ __global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
     qf[s] = as_bf16x8(ld16(p.q + qrow * p.qs + head * p.qh + 16 * s + 8 * hi));
     dof[s] = as_bf16x8(ld16(p.dout + qrow * p.dos + head * p.doh + 16 * s + 8 * hi));
   }
-  const float* rec = p.stats + (head * 2 * p.n_q_tiles + 2 * r + (qg >> 1)) * kRecFloats;
-  const float lse2 = rec[(32 * qg + li) & 63];
-  const float dq_d = rec[64 + ((32 * qg + li) & 63)];
+  const float* rec = p.stats + (head * 2 * p.n_q_tiles + 2 * r + (wave >> 1)) * kRecFloats;
+  const float lse2 = rec[(32 * wave + li) & 63];
+  const float dq_d = rec[64 + ((32 * wave + li) & 63)];
   f32x16 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -282,14 +282,13 @@ __global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
 
   const uint16_t* kbase = p.k + head * p.kh;
   const uint16_t* vbase = p.v + head * p.vh;
-  uint32_t koff[2], voff[2];
+  uint32_t koff[4], voff[4];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    koff[u] = seg_offset(2 * wave + u, lane, p.ks);
-    voff[u] = seg_offset(2 * wave + u, lane, p.vs);
+  for (int u = 0; u < 4; ++u) {
+    koff[u] = seg_offset(4 * wave + u, lane, p.ks);
+    voff[u] = seg_offset(4 * wave + u, lane, p.vs);
   }
   const Frag f = frag_offsets(lane);
-  const uint32_t kb32 = 32 * kh * 256;  // this wave's keys inside a step
   const float c = p.scale_log2;
 
   auto load_step = [&](int u, lds_u8* slot) {
@@ -298,18 +297,15 @@ __global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
     const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
     const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      dma16(kb, koff[s], slot + (2 * wave + s) * 1024);
-      dma16(vb, voff[s], slot + kHalfBytes + (2 * wave + s) * 1024);
+    for (int s = 0; s < 4; ++s) {
+      dma16(kb, koff[s], slot + (4 * wave + s) * 1024);
+      dma16(vb, voff[s], slot + kHalfBytes + (4 * wave + s) * 1024);
     }
   };
-  auto compute = [&](int u, const lds_u8* slot) {
-    const int t = __builtin_amdgcn_readfirstlane(steps[u]);
-    const int vc = __builtin_amdgcn_readfirstlane((int)tvc[t >> 1]);
-    const int lim = (t & 1 ? vc - kHalf : min(vc, kHalf)) - 32 * kh;  // valid keys of this wave
-    if (lim <= 0) return;
-    const lds_u8* ks = slot + kb32;
-    const lds_u8* vs = slot + kHalfBytes + kb32;
+  // One 32-key half kh of a step with `lim` valid keys in it (lim >= 32: all).
+  auto half_step = [&](const lds_u8* slot, int kh, int lim) {
+    const lds_u8* ks = slot + kh * 32 * 256;
+    const lds_u8* vs = slot + kHalfBytes + kh * 32 * 256;
     f32x16 st, dp;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -325,9 +321,9 @@ __global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
     float ds[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      float pr = __builtin_amdgcn_exp2f(fmaf(st[e], c, -lse2));
-      if (lim < 32 && 8 * (e >> 2) + 4 * hi + (e & 3) >= lim) pr = 0.f;
-      ds[e] = pr * (dp[e] - dq_d);
+      const float pr = __builtin_amdgcn_exp2f(fmaf(st[e], c, -lse2));
+      const float x = pr * (dp[e] - dq_d);
+      ds[e] = (lim < 32 && 8 * (e >> 2) + 4 * hi + (e & 3) >= lim) ? 0.f : x;
     }
     u32x4 pk[2];
     pack_b(ds, pk);
@@ -337,6 +333,13 @@ __global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
       for (int dt = 0; dt < 4; ++dt)
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag(ks, f, dt, kk), as_bf16x8(pk[kk]),
                                                           acc[dt], 0, 0, 0);
+  };
+  auto compute = [&](int u, const lds_u8* slot) {
+    const int t = __builtin_amdgcn_readfirstlane(steps[u]);
+    const int vc = __builtin_amdgcn_readfirstlane((int)tvc[t >> 1]);
+    const int vch = t & 1 ? vc - kHalf : min(vc, kHalf);  // valid keys of the step
+    half_step(slot, 0, vch);
+    if (vch > 32) half_step(slot, 1, vch - 32);
   };
 
   lds_u8* s0 = (lds_u8*)ring[0];
@@ -358,26 +361,11 @@ __global__ void __launch_bounds__(kDqThreads) dq_kernel(BwdParams p) {
     run(u + 1, s1, s0);
   }
 
-  // Sum the two key halves: waves 4..7 park their accumulators in the ring.
-  __syncthreads();
-  lds_f32* buf = (lds_f32*)ring[0];
-  if (kh == 1) {
+  uint16_t* drow = p.dq + qrow * p.dqs + head * p.dqh;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) buf[(qg * 64 + dt * 16 + e) * 64 + lane] = acc[dt][e];
-  }
-  __syncthreads();
-  if (kh == 0) {
-    uint16_t* drow = p.dq + qrow * p.dqs + head * p.dqh;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[dt][e] += buf[(qg * 64 + dt * 16 + e) * 64 + lane];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) store4(drow, 32 * dt + 8 * g + 4 * hi, acc[dt], 4 * g, p.scale);
-    }
-  }
+    for (int g = 0; g < 4; ++g) store4(drow, 32 * dt + 8 * g + 4 * hi, acc[dt], 4 * g, p.scale);
 }
 
 // ---------------------------------------------------------------------------
