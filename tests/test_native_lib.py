@@ -77,6 +77,18 @@ def test_host_side_argument_checks():
         _native.call('veda_block_sparse_bwd', *([16, 0, 0] * 5), 16, 0, 0, None, 0, 0, 1, 128,
                      1, 1, None, None, None, None, 1, None, None, None, None, 1, None, 1.0,
                      *([16, 0, 0] * 3), 16, 1024, 0, None)
+    with pytest.raises(ValueError, match='head_dim'):
+        _native.call('veda_compensated_attention', None, 0, 0, None, 0, 0, None, 0, 0, 1, 64, 1, 1,
+                     None, None, None, None, 1, None, None, 0, 0, None, None, 1.0, None, 0, 0, 0,
+                     None)
+    with pytest.raises(ValueError, match='front_tiles'):
+        _native.call('veda_compensated_attention', None, 0, 0, None, 0, 0, None, 0, 0, 1, 128, 1,
+                     1, None, None, None, None, 1, None, None, 0, 0, None, None, 1.0, None, 0, 0,
+                     -1, None)
+    with pytest.raises(ValueError, match='front_tiles'):
+        _native.call('veda_block_sparse_bwd', *([16, 0, 0] * 5), 16, 0, 0, None, 0, 0, 1, 128,
+                     2, 1, None, None, None, None, 2, None, None, None, None, 2, None, 1.0,
+                     *([16, 0, 0] * 3), 16, 1 << 20, 2, None)
     with pytest.raises(ValueError, match='reduce'):
         _native.call('veda_heat_combine', None, None, 0, 0, None, None, 1, 1, 1, 5, None, None)
     assert isinstance(lib.veda_last_error(), bytes)
