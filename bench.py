@@ -356,9 +356,6 @@ def main() -> int:
               'shares -- run with --gpus 1', file=sys.stderr)
         return 2
     from miowtion_amd import kernels, mask as pm
-    if args.suite:
-        print(json.dumps({'suite': suite(), 'gpu': torch.cuda.get_device_name(0)}), flush=True)
-        return 0
     if args.copy_bytes:
         n = args.copy_bytes // 4
         src = torch.ones(n, dtype=torch.float32, device='cuda')
@@ -368,6 +365,9 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
         _log(f'bench: copied {args.copy_bytes} bytes x 3 (counter calibration)')
+    if args.suite:
+        print(json.dumps({'suite': suite(), 'gpu': torch.cuda.get_device_name(0)}), flush=True)
+        return 0
     _log('bench: building C2 case')
     c = build_case()
     lay = c['lay']

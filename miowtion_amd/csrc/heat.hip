@@ -1,18 +1,20 @@
 // Teacher block heat for gfx950: per (head, query tile, key tile) the block's
 // softmax mass ('sum') or peak probability ('max') from the dense LSE.
 //
-// Workgroup = (head, query tile): 8 waves walk every key tile of the head
-// through the same pipeline as the attention kernel, with K only: 64-key
-// steps in a 4-slot LDS ring (three steps in flight), padding rows (past a
-// tile's valid count) not fetched, an upper half with no valid key no step
-// at all. Wave w = (query group qg = w & 3: rows 32 qg .. + 31, key half
-// kh = w >> 2: keys 32 kh .. + 31 of every step) keeps its rows' Q^T in
-// registers as the B operand of S^T = K Q^T (v_mfma_f32_32x32x16_bf16), so
-// each lane holds one query row and 16 keys of a step. A step's contribution
-// is reduced over the wave (DPP and lane swaps, no LDS round trip) and added
-// (or max-ed) into the wave's own LDS slot for that key tile; the eight
-// waves' slots are combined in a fixed order at the end, so the result does
-// not depend on timing. Only one fp32 value per block leaves the workgroup.
+// Workgroup = (head, pair of query items): 8 waves walk every key tile of the
+// head once, so each K tile fetched into LDS serves two query tiles. Wave w
+// owns query item w / 4 of the pair and its rows 32 (w % 4) .. + 31, and all
+// 64 keys of every step (two 32-key sub-blocks). Steps are 64-key halves of
+// the key tiles in tile order (a tile's halves consecutive; rows past its
+// valid count not fetched, an empty half no step), through a 4-slot LDS ring
+// with three steps in flight. Each wave keeps its rows' Q^T in registers as
+// the B operand of S^T = K Q^T (v_mfma_f32_32x32x16_bf16), so a lane holds
+// one query row and 16 keys of a sub-block; a lane accumulates its share of
+// the current key tile in a register and the wave reduces it (DPP and lane
+// swaps) once, at the tile's last step, into its own LDS slot for the tile.
+// The four waves of an item are combined in a fixed order at the end, so
+// the result does not depend on timing. Only one fp32 value per block
+// leaves the workgroup.
 
 #include "veda_common.h"
 #include "veda_pipeline.h"
@@ -65,7 +67,8 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t kr1[kHalfBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t kr2[kHalfBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t kr3[kHalfBytes];
-  __shared__ int32_t step_list[2 * kMaxTiles];
+  __shared__ uint16_t steps[2 * kMaxTiles];  // (key tile << 2) | (half << 1) | last of tile
+  __shared__ uint8_t tvc[kMaxTiles];
   __shared__ float part[8][kMaxTiles];
   __shared__ int32_t step_total;
   lds_u8* K0 = (lds_u8*)kr0;
@@ -74,54 +77,46 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
   lds_u8* K3 = (lds_u8*)kr3;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int qg = wave & 3, kh = wave >> 2;
+  const int pick = wave >> 2, rg = wave & 3;  // item of the pair, row group
   const int li = lane & 31, hi = lane >> 5;
-  const int64_t item = blockIdx.x;
-  const int64_t head = item / p.n_q;
-  const int64_t r = item % p.n_q;
-  const int64_t qt = p.q_tiles[r];
+  const int64_t n_pairs = (p.n_q + 1) / 2;
+  const int64_t head = blockIdx.x / n_pairs;
+  const int64_t r = (blockIdx.x % n_pairs) * 2 + pick;
   const int nt = (int)p.n_tiles;
-  float* heat_row = p.heat + (head * p.n_q + r) * p.n_tiles;
-  if (qt < 0 || qt >= p.n_tiles) {  // not a query tile of this layout: no heat
-    for (int j = tid; j < nt; j += kHeatThreads) heat_row[j] = 0.f;
-    return;
-  }
+  const bool item_ok = r < p.n_q;
+  const int64_t qt = item_ok ? p.q_tiles[r] : -1;
+  const bool qt_ok = qt >= 0 && qt < p.n_tiles;
 
-  // Zero the ring (stale rows only ever meet masked keys), reset the
-  // partials, and build the step list: (key tile << 8) | (half << 7) | valid
-  // keys of the half; first halves of all tiles in tile order, then the
-  // second halves of tiles with more than 64 valid keys (ranked by a ballot).
-  for (int i = tid; i < kHalfBytes / 16; i += kHeatThreads) {
-    const u32x4 z = {0, 0, 0, 0};
-    reinterpret_cast<u32x4*>(kr0)[i] = z;
-    reinterpret_cast<u32x4*>(kr1)[i] = z;
-    reinterpret_cast<u32x4*>(kr2)[i] = z;
-    reinterpret_cast<u32x4*>(kr3)[i] = z;
-  }
+  // Partials start empty (a tile no step reaches keeps them); the step
+  // list is built by wave 0: every tile with a valid key, its first half and
+  // then its second half when more than 64 keys are valid, in tile order
+  // (positions from a ballot prefix).
   for (int j = tid; j < nt; j += kHeatThreads) {
+    tvc[j] = (uint8_t)min(max(p.valid_count[j], 0), kTile);
 #pragma unroll
     for (int w = 0; w < 8; ++w) part[w][j] = REDUCE ? -INFINITY : 0.f;
-    step_list[j] = (j << 8) | min(max(p.valid_count[j], 0), kHalf);
   }
   if (wave == 0) {
-    int h1 = 0;
+    int n = 0;
     for (int j0 = 0; j0 < nt; j0 += 64) {
       const int j = j0 + lane;
-      const int vc = j < nt ? min(p.valid_count[j], kTile) : 0;
-      const bool two = vc > kHalf;
-      const uint64_t bal = __ballot(two);
-      const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
-      if (two) step_list[nt + h1 + rank] = (j << 8) | (1 << 7) | (vc - kHalf);
-      h1 += __builtin_popcountll(bal);
+      const int vc = j < nt ? min(max(p.valid_count[j], 0), kTile) : 0;
+      const bool one = vc > 0, two = vc > kHalf;
+      const uint64_t b1 = __ballot(one), b2 = __ballot(two);
+      const int rank =
+          __builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0)) +
+          __builtin_amdgcn_mbcnt_hi((uint32_t)(b2 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b2, 0));
+      if (one) steps[n + rank] = (uint16_t)((j << 2) | (two ? 0 : 1));
+      if (two) steps[n + rank + 1] = (uint16_t)((j << 2) | 2 | 1);
+      n += __builtin_popcountll(b1) + __builtin_popcountll(b2);
     }
-    if (lane == 0) step_total = nt + h1;
+    if (lane == 0) step_total = n;
   }
 
-  const int vcq = min(max(p.valid_count[qt], 0), kTile);
-  const int row = 32 * qg + li;
+  const int vcq = qt_ok ? min(max(p.valid_count[qt], 0), kTile) : 0;
+  const int row = 32 * rg + li;
   const bool row_ok = row < vcq;
-  const int64_t qrow = qt * kTile + row;
+  const int64_t qrow = (qt_ok ? qt : 0) * kTile + row;
   bf16x8 qf[8];
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
@@ -135,22 +130,26 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
   // sum: exp2(s * c2 - lse2); an invalid row has lse2 = +inf (adds 0).
   const float c2 = p.scale * kLog2e;
   const float lse2 = row_ok ? lse * kLog2e : INFINITY;
-  __syncthreads();  // ring, partials and step list ready
+  __syncthreads();  // partials, valid counts and step list ready
   const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
 
-  uint32_t kfo[8];  // K fragment offsets: row 32 kh + li, logical chunk 2s + hi
+  uint32_t kfo[8];  // K fragment offsets: row li (+ 32 sub-block), logical chunk 2s + hi
   {
-    const uint32_t krow = (32 * kh + li) * 256, x = (hi ^ (li & 15)) << 4;
+    const uint32_t krow = li * 256, x = (hi ^ (li & 15)) << 4;
 #pragma unroll
     for (int s = 0; s < 8; ++s) kfo[s] = krow + (x ^ (s << 5));
   }
   const KDma dma = kdma_offsets(p.ks, wave, lane);
   const uint16_t* kbase = p.k + head * p.kh;
-  auto word = [&](int u) { return __builtin_amdgcn_readfirstlane(step_list[u]); };
+  auto entry = [&](int u) { return __builtin_amdgcn_readfirstlane((int)steps[u]); };
+  auto valid_of = [&](int e) {  // valid keys of the step's half
+    const int vc = __builtin_amdgcn_readfirstlane((int)tvc[e >> 2]);
+    return (e & 2) ? vc - kHalf : min(vc, kHalf);
+  };
   auto load_step = [&](int u, lds_u8* slot) {
-    const int wd = word(u);
-    const int64_t row0 = (int64_t)(wd >> 8) * kTile + ((wd >> 7) & 1) * kHalf;
-    const int vch = wd & 127;
+    const int e = entry(u);
+    const int64_t row0 = (int64_t)(e >> 2) * kTile + ((e >> 1) & 1) * kHalf;
+    const int vch = valid_of(e);
     const char* b = reinterpret_cast<const char*>(kbase + row0 * p.ks);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -158,14 +157,13 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
       dma16(b, 4 * seg < vch ? dma.k[s] : dma.skip[s], slot + seg * 1024);
     }
   };
-  auto compute_step = [&](int u, const lds_u8* slot) {
-    const int wd = word(u);
-    const int j = wd >> 8, vch = wd & 127;
-    if (vch <= 32 * kh) return;  // this wave's 32 keys are all padding
+  float acc = REDUCE ? -INFINITY : 0.f;  // this lane's share of the current key tile
+  // One 32-key sub-block (keys kb .. kb + 31 of the half, lim of them valid).
+  auto sub_block = [&](const lds_u8* slot, int kb, int lim) {
     u32x4 kf[8];
 #pragma unroll
     for (int s = 0; s < 8; ++s)
-      kf[s] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(slot + kfo[s]);
+      kf[s] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(slot + kb * 256 + kfo[s]);
     f32x16 sacc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
@@ -173,24 +171,16 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
     for (int s = 0; s < 8; ++s)
       sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kf[s]), qf[s],
                                                      sacc, 0, 0, 0);
-    // Register e holds key 32 kh + 8 (e / 4) + 4 hi + e % 4 of the half.
-    if (vch < 32 * (kh + 1)) {
-      const int lim = vch - 32 * kh - 4 * hi;
+    // Register e holds key kb + 8 (e / 4) + 4 hi + e % 4 of the half.
+    if (lim < 32) {
+      const int l = lim - 4 * hi;
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        if (8 * (e >> 2) + (e & 3) >= lim) sacc[e] = -INFINITY;
+        if (8 * (e >> 2) + (e & 3) >= l) sacc[e] = -INFINITY;
     }
-    float v;
     if (REDUCE) {
-      // Row max over the step's keys, rounded to bf16 like the reference's
-      // bf16 scores (rounding is monotonic, so rounding the max is rounding
-      // every score), then max over rows of max * scale - lse.
-      float rm = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) rm = fmaxf(rm, sacc[e]);
-      if (rm != -INFINITY) rm = bf16_to_f32(f32_to_bf16(rm));
-      v = (rm == -INFINITY || !row_ok) ? -INFINITY : rm * p.scale - lse;
-      v = wave_reduce<true>(v);
+      for (int e = 0; e < 16; ++e) acc = fmaxf(acc, sacc[e]);
     } else {
       float a[4];
 #pragma unroll
@@ -199,14 +189,38 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) a[g] += __builtin_amdgcn_exp2f(fmaf(sacc[4 * g + m], c2, -lse2));
       }
-      v = wave_reduce<false>((a[0] + a[1]) + (a[2] + a[3]));
+      acc += (a[0] + a[1]) + (a[2] + a[3]);
     }
-    if (lane == 0) part[wave][j] = REDUCE ? fmaxf(part[wave][j], v) : part[wave][j] + v;
+  };
+  auto compute_step = [&](int u, const lds_u8* slot) {
+    const int e = entry(u);
+    const int vch = valid_of(e);
+    sub_block(slot, 0, vch);
+    if (vch > 32) sub_block(slot, 32, vch - 32);
+    if (e & 1) {  // the tile's last step: reduce over the wave into its slot
+      float v;
+      if (REDUCE) {
+        // Row max over the tile's keys, rounded to bf16 like the
+        // reference's bf16 scores (rounding is monotonic, so rounding the
+        // max is rounding every score), then max over rows of
+        // max * scale - lse.
+        float rm = half_swap_max(acc);
+        if (rm != -INFINITY) rm = bf16_to_f32(f32_to_bf16(rm));
+        v = (rm == -INFINITY || !row_ok) ? -INFINITY : rm * p.scale - lse;
+        v = wave_reduce<true>(v);
+      } else {
+        v = wave_reduce<false>(acc);
+      }
+      if (lane == 0) part[wave][e >> 2] = v;
+      acc = REDUCE ? -INFINITY : 0.f;
+    }
   };
   // The ring: step u in slot u & 3; at the top of step u its own two loads
   // per wave are waited for (those of u+1, u+2 may stay in flight), then a
   // bare barrier (as in the attention kernel), then the slot step u-1 used is
-  // refilled with step u+3.
+  // refilled with step u+3. Every row of a slot that a step reads was
+  // written by that step's loads (segments past the valid count re-read
+  // real rows).
   auto top = [&](int u) {
     if (u + 2 < n_steps) VEDA_WAIT_VM(4);
     else if (u + 1 < n_steps) VEDA_WAIT_VM(2);
@@ -234,12 +248,21 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
     compute_step(u + 3, K3);
   }
   __syncthreads();  // all partials written
-  for (int j = tid; j < nt; j += kHeatThreads) {
-    float v = part[0][j];
+  // each item's four waves, in order
 #pragma unroll
-    for (int w = 1; w < 8; ++w) v = REDUCE ? fmaxf(v, part[w][j]) : v + part[w][j];
-    if (REDUCE) v = v == -INFINITY ? 0.f : expf(v);
-    heat_row[j] = v;
+  for (int it = 0; it < 2; ++it) {
+    const int64_t rr = (blockIdx.x % n_pairs) * 2 + it;
+    if (rr >= p.n_q) break;
+    const int64_t qti = p.q_tiles[rr];
+    const bool ok = qti >= 0 && qti < p.n_tiles;  // not a query tile of this layout: no heat
+    float* heat_row = p.heat + (head * p.n_q + rr) * p.n_tiles;
+    for (int j = tid; j < nt; j += kHeatThreads) {
+      float v = part[4 * it][j];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) v = REDUCE ? fmaxf(v, part[4 * it + w][j]) : v + part[4 * it + w][j];
+      if (REDUCE) v = v == -INFINITY ? 0.f : expf(v);
+      heat_row[j] = ok ? v : 0.f;
+    }
   }
 }
 
@@ -320,7 +343,7 @@ extern "C" int veda_block_heat(const void* q, int64_t q_stride_s, int64_t q_stri
   p.valid_count = valid_count; p.q_tiles = q_tiles;
   p.n_q = n_q; p.n_tiles = n_tiles; p.n_heads = n_heads;
   p.scale = scale; p.heat = heat;
-  const int64_t items = n_heads * n_q;
+  const int64_t items = n_heads * ((n_q + 1) / 2);  // a workgroup per pair of query items
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (reduce) heat_kernel<1><<<(unsigned)items, kHeatThreads, 0, s>>>(p);
   else heat_kernel<0><<<(unsigned)items, kHeatThreads, 0, s>>>(p);
