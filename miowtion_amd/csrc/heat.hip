@@ -1,18 +1,19 @@
 // Teacher block heat for gfx950: per (head, query tile, key tile) the block's
 // softmax mass ('sum') or peak probability ('max') from the dense LSE.
 //
-// Workgroup = (head, pair of query items): 8 waves walk every key tile of the
-// head once, so each K tile fetched into LDS serves two query tiles. Wave w
-// owns query item w / 4 of the pair and its rows 32 (w % 4) .. + 31, and all
-// 64 keys of every step (two 32-key sub-blocks). Steps are 64-key halves of
+// Workgroup = (head, group of four query items): 16 waves walk every key tile
+// of the head once, so each K tile fetched into LDS serves four query tiles.
+// Wave w owns query item w / 4 of the group and its rows 32 (w % 4) .. + 31,
+// and all 64 keys of every step (two 32-key sub-blocks). Steps are 64-key halves of
 // the key tiles in tile order (a tile's halves consecutive; rows past its
 // valid count not fetched, an empty half no step), through a 4-slot LDS ring
 // with three steps in flight. Each wave keeps its rows' Q^T in registers as
 // the B operand of S^T = K Q^T (v_mfma_f32_32x32x16_bf16), so a lane holds
 // one query row and 16 keys of a sub-block; a lane accumulates its share of
 // the current key tile in a register and the wave reduces it (DPP and lane
-// swaps) once, at the tile's last step, into its own LDS slot for the tile.
-// The four waves of an item are combined in a fixed order at the end, so
+// swaps) once, at the tile's last step, into an LDS table (two of them,
+// alternating); after the next barrier the first wave of each item adds the
+// item's four entries in a fixed order into the item's slot for the tile, so
 // the result does not depend on timing. Only one fp32 value per block
 // leaves the workgroup.
 
@@ -23,7 +24,8 @@ namespace veda {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kHeatThreads = 512;
+constexpr int kHeatThreads = 1024;
+constexpr int kHeatItems = 4;  // query items per workgroup
 constexpr int kMaxTiles = 2048;  // key tiles per layout (FA4's block-mask cap)
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -40,25 +42,19 @@ struct HeatParams {
   float* heat;
 };
 
-// Per-lane byte offsets of this wave's two 1 KB K segments of a step (rows
-// 4 seg + l / 16, LDS chunk l % 16 holding logical chunk (l % 16) ^ (row &
-// 15)) and of their redirect (rows l / 16) for segments wholly past the
-// valid count.
+// Per-lane byte offsets of this wave's 1 KB K segment of a step (segment =
+// wave: rows 4 wave + l / 16, LDS chunk l % 16 holding logical chunk
+// (l % 16) ^ (row & 15)) and of its redirect (rows l / 16) for a segment
+// wholly past the valid count.
 struct KDma {
-  uint32_t k[2], skip[2];
+  uint32_t k, skip;
 };
 
 __device__ __forceinline__ KDma kdma_offsets(int64_t ks, int wave, int lane) {
-  KDma d;
   const int lr = lane >> 4, pc = lane & 15;
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int row = 4 * (2 * wave + u) + lr;
-    const int kc = (pc ^ (row & 15)) << 3;
-    d.k[u] = (uint32_t)((row * ks + kc) * 2);
-    d.skip[u] = (uint32_t)((lr * ks + kc) * 2);
-  }
-  return d;
+  const int row = 4 * wave + lr;
+  const int kc = (pc ^ (row & 15)) << 3;
+  return KDma{(uint32_t)((row * ks + kc) * 2), (uint32_t)((lr * ks + kc) * 2)};
 }
 
 template <int REDUCE>  // 0: sum, 1: max
@@ -69,7 +65,8 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t kr3[kHalfBytes];
   __shared__ uint16_t steps[2 * kMaxTiles];  // (key tile << 2) | (half << 1) | last of tile
   __shared__ uint8_t tvc[kMaxTiles];
-  __shared__ float part[8][kMaxTiles];
+  __shared__ float part[kHeatItems][kMaxTiles];
+  __shared__ float tilebuf[2][16];  // per wave, a key tile's reduced share; two tables, alternating
   __shared__ int32_t step_total;
   lds_u8* K0 = (lds_u8*)kr0;
   lds_u8* K1 = (lds_u8*)kr1;
@@ -79,9 +76,9 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int pick = wave >> 2, rg = wave & 3;  // item of the pair, row group
   const int li = lane & 31, hi = lane >> 5;
-  const int64_t n_pairs = (p.n_q + 1) / 2;
-  const int64_t head = blockIdx.x / n_pairs;
-  const int64_t r = (blockIdx.x % n_pairs) * 2 + pick;
+  const int64_t n_groups = (p.n_q + kHeatItems - 1) / kHeatItems;
+  const int64_t head = blockIdx.x / n_groups;
+  const int64_t r = (blockIdx.x % n_groups) * kHeatItems + pick;
   const int nt = (int)p.n_tiles;
   const bool item_ok = r < p.n_q;
   const int64_t qt = item_ok ? p.q_tiles[r] : -1;
@@ -94,7 +91,7 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
   for (int j = tid; j < nt; j += kHeatThreads) {
     tvc[j] = (uint8_t)min(max(p.valid_count[j], 0), kTile);
 #pragma unroll
-    for (int w = 0; w < 8; ++w) part[w][j] = REDUCE ? -INFINITY : 0.f;
+    for (int it = 0; it < kHeatItems; ++it) part[it][j] = REDUCE ? -INFINITY : 0.f;
   }
   if (wave == 0) {
     int n = 0;
@@ -151,13 +148,22 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
     const int64_t row0 = (int64_t)(e >> 2) * kTile + ((e >> 1) & 1) * kHalf;
     const int vch = valid_of(e);
     const char* b = reinterpret_cast<const char*>(kbase + row0 * p.ks);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int seg = 2 * wave + s;
-      dma16(b, 4 * seg < vch ? dma.k[s] : dma.skip[s], slot + seg * 1024);
-    }
+    dma16(b, 4 * wave < vch ? dma.k : dma.skip, slot + wave * 1024);
   };
   float acc = REDUCE ? -INFINITY : 0.f;  // this lane's share of the current key tile
+  // (wave-uniform) key tile whose table entries wait for the combine, the
+  // table they are in, and the number of tiles ended so far
+  int pend = -1, pend_tab = 0, ends = 0;
+  auto combine = [&]() {
+    if (pend >= 0 && rg == 0 && lane == 0) {
+      const float* t = tilebuf[pend_tab] + 4 * pick;
+      float v = t[0];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) v = REDUCE ? fmaxf(v, t[w]) : v + t[w];
+      part[pick][pend] = v;
+    }
+    pend = -1;
+  };
   // One 32-key sub-block (keys kb .. kb + 31 of the half, lim of them valid).
   auto sub_block = [&](const lds_u8* slot, int kb, int lim) {
     u32x4 kf[8];
@@ -193,6 +199,7 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
     }
   };
   auto compute_step = [&](int u, const lds_u8* slot) {
+    combine();  // the previous tile's entries are visible after this step's barrier
     const int e = entry(u);
     const int vch = valid_of(e);
     sub_block(slot, 0, vch);
@@ -211,20 +218,26 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
       } else {
         v = wave_reduce<false>(acc);
       }
-      if (lane == 0) part[wave][e >> 2] = v;
+      // consecutive tile ends alternate tables, so a table is written again
+      // only after the barrier that follows its combine
+      pend_tab = ends & 1;
+      ++ends;
+      if (lane == 0) tilebuf[pend_tab][wave] = v;
+      pend = e >> 2;
       acc = REDUCE ? -INFINITY : 0.f;
     }
   };
-  // The ring: step u in slot u & 3; at the top of step u its own two loads
-  // per wave are waited for (those of u+1, u+2 may stay in flight), then a
-  // bare barrier (as in the attention kernel), then the slot step u-1 used is
-  // refilled with step u+3. Every row of a slot that a step reads was
-  // written by that step's loads (segments past the valid count re-read
-  // real rows).
+  // The ring: step u in slot u & 3; at the top of step u its own load is
+  // waited for (those of u+1, u+2 may stay in flight) together with this
+  // wave's LDS stores (the tile table), then a bare barrier (as in the
+  // attention kernel), then the slot step u-1 used is refilled with step
+  // u+3. Every row of a slot that a step reads was written by that step's
+  // loads (segments past the valid count re-read real rows).
   auto top = [&](int u) {
-    if (u + 2 < n_steps) VEDA_WAIT_VM(4);
-    else if (u + 1 < n_steps) VEDA_WAIT_VM(2);
-    else VEDA_WAIT_VM(0);
+    // s_waitcnt vmcnt(n) lgkmcnt(0)
+    if (u + 2 < n_steps) __builtin_amdgcn_s_waitcnt(0x0070 | 2);
+    else if (u + 1 < n_steps) __builtin_amdgcn_s_waitcnt(0x0070 | 1);
+    else __builtin_amdgcn_s_waitcnt(0x0070);
     __builtin_amdgcn_s_barrier();
   };
   if (n_steps > 0) load_step(0, K0);
@@ -247,19 +260,18 @@ __global__ void __launch_bounds__(kHeatThreads) heat_kernel(HeatParams p) {
     if (u + 6 < n_steps) load_step(u + 6, K2);
     compute_step(u + 3, K3);
   }
+  __syncthreads();  // the last tile's table entries written
+  combine();
   __syncthreads();  // all partials written
-  // each item's four waves, in order
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int64_t rr = (blockIdx.x % n_pairs) * 2 + it;
+  for (int it = 0; it < kHeatItems; ++it) {
+    const int64_t rr = (blockIdx.x % n_groups) * kHeatItems + it;
     if (rr >= p.n_q) break;
     const int64_t qti = p.q_tiles[rr];
     const bool ok = qti >= 0 && qti < p.n_tiles;  // not a query tile of this layout: no heat
     float* heat_row = p.heat + (head * p.n_q + rr) * p.n_tiles;
     for (int j = tid; j < nt; j += kHeatThreads) {
-      float v = part[4 * it][j];
-#pragma unroll
-      for (int w = 1; w < 4; ++w) v = REDUCE ? fmaxf(v, part[4 * it + w][j]) : v + part[4 * it + w][j];
+      float v = part[it][j];
       if (REDUCE) v = v == -INFINITY ? 0.f : expf(v);
       heat_row[j] = ok ? v : 0.f;
     }
@@ -343,7 +355,7 @@ extern "C" int veda_block_heat(const void* q, int64_t q_stride_s, int64_t q_stri
   p.valid_count = valid_count; p.q_tiles = q_tiles;
   p.n_q = n_q; p.n_tiles = n_tiles; p.n_heads = n_heads;
   p.scale = scale; p.heat = heat;
-  const int64_t items = n_heads * ((n_q + 1) / 2);  // a workgroup per pair of query items
+  const int64_t items = n_heads * ((n_q + kHeatItems - 1) / kHeatItems);  // per group of items
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (reduce) heat_kernel<1><<<(unsigned)items, kHeatThreads, 0, s>>>(p);
   else heat_kernel<0><<<(unsigned)items, kHeatThreads, 0, s>>>(p);
