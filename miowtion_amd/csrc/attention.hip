@@ -1,7 +1,9 @@
 // Flash-attention forwards for gfx950 (head_dim 128, bf16 in, fp32
 // accumulate). Two kernels share the step, fragment and load code below:
-//   hfwd_kernel  the teacher's pass over all key tiles in tile order (block
-//                heat statistics, optionally the dense output);
+//   hfwd_kernel  the teacher's pass over all key tiles in tile order with
+//                the dense output (and the block heat statistics);
+//   tstats_kernel the same pass without the output (LSE and statistics
+//                only), four query tiles per K pass;
 //   sfwd_kernel  the block-sparse forward, the zero-order compensation and
 //                the dense forward of packed rows (two 4-wave workgroups
 //                per CU, described at its section).
@@ -1035,6 +1037,188 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
         !row_real ? 0.f : l > 0.f ? (w.m_run + __log2f(l)) * kLn2 : -INFINITY;
 }
 
+// ---------------------------------------------------------------------------
+// Teacher statistics pass (no dense output): the LSE of every query row over
+// all valid keys, and per (key tile, row) the block statistic of the heat.
+//
+// Workgroup = (head, group of four query items), 16 waves, so each K tile
+// fetched into LDS serves four query tiles. Wave w owns item w / 4 of the
+// group, rows 32 (w % 4) .. + 31 (Q^T in registers), and all 64 keys of every
+// step (two 32-key sub-blocks): the same online softmax as the sparse
+// forward's (log2 domain, reference max raised only past a slack of 8), with
+// the current key tile's partial (sum relative to the reference, or the raw
+// max) in a register, written as one log2 statistic per row at the tile's
+// last step. Steps are the 64-key halves of every key tile in tile order, a
+// tile's halves consecutive (an empty tile one step with no valid key, so
+// every tile gets its statistic), through a 4-slot K ring.
+
+constexpr int kStatThreads = 1024;
+constexpr int kStatItems = 4;
+
+template <int HEAT>
+__global__ void __launch_bounds__(kStatThreads) tstats_kernel(FwdParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[4][kHalfBytes];
+  __shared__ uint16_t steps[2 * kMaxBlocks];  // (key tile << 2) | (half << 1) | last of tile
+  __shared__ uint8_t tvc[kMaxBlocks];
+  __shared__ int32_t step_total;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int pick = wave >> 2, rg = wave & 3;
+  const int li = lane & 31, hi = lane >> 5;
+  const int64_t n_groups = (p.n_q_tiles + kStatItems - 1) / kStatItems;
+  const int64_t head = blockIdx.x / n_groups;
+  const int64_t r = (blockIdx.x % n_groups) * kStatItems + pick;
+  const bool item_ok = r < p.n_q_tiles;
+  const int64_t qrow = r * kTile + 32 * rg + li;  // row of lse / part
+  const int64_t qtile = item_ok ? (p.q_tiles != nullptr ? p.q_tiles[r] : r) : -1;
+  const bool qtile_ok = qtile >= 0 && qtile < p.q_tiles_held;
+  const int64_t qsrc = (qtile_ok ? qtile : 0) * kTile + 32 * rg + li;
+  const int nk = (int)p.n_k_tiles;
+
+  for (int j = tid; j < nk; j += kStatThreads) tvc[j] = (uint8_t)min(max(p.valid_count[j], 0), kTile);
+  if (wave == 0) {
+    int n = 0;
+    for (int j0 = 0; j0 < nk; j0 += 64) {
+      const int j = j0 + lane;
+      const bool one = j < nk;
+      const bool two = one && p.valid_count[j] > kHalf;
+      const uint64_t b1 = __ballot(one), b2 = __ballot(two);
+      const int rank =
+          __builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0)) +
+          __builtin_amdgcn_mbcnt_hi((uint32_t)(b2 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b2, 0));
+      if (one) steps[n + rank] = (uint16_t)((j << 2) | (two ? 0 : 1));
+      if (two) steps[n + rank + 1] = (uint16_t)((j << 2) | 2 | 1);
+      n += __builtin_popcountll(b1) + __builtin_popcountll(b2);
+    }
+    if (lane == 0) step_total = n;
+  }
+
+  WaveState w;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const u32x4 v =
+        qtile_ok ? ld16(p.q + qsrc * p.qs + head * p.qh + 16 * s + 8 * hi) : u32x4{0, 0, 0, 0};
+    w.qf[s] = as_bf16x8(v);
+  }
+#pragma unroll
+  for (int s = 0; s < 8; ++s) asm volatile("" : : "v"(w.qf[s]));
+  w.m_run = -INFINITY;
+  w.l_run = 0.f;
+  w.mu = 0.f;
+  w.blk = HEAT == kHeatMax ? -INFINITY : 0.f;
+  __syncthreads();  // step list and valid counts ready
+  const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
+
+  const float c = p.scale_log2;
+  const HFrag fa = hfrag_offsets(0, lane), fb = hfrag_offsets(1, lane);
+  // this wave's 1 KB K segment of a step: rows 4 wave + lane / 16, LDS chunk
+  // lane % 16 holding logical chunk (lane % 16) ^ (row & 15); a segment
+  // wholly past the valid count re-reads rows lane / 16
+  uint32_t koff, kskip;
+  {
+    const int lr = lane >> 4, pc = lane & 15, row = 4 * wave + lr;
+    const int kc = (pc ^ (row & 15)) << 3;
+    koff = (uint32_t)((row * p.ks + kc) * 2);
+    kskip = (uint32_t)((lr * p.ks + kc) * 2);
+  }
+  const uint16_t* kbase = p.k + head * p.kh;
+  auto entry = [&](int u) { return __builtin_amdgcn_readfirstlane((int)steps[u]); };
+  auto valid_of = [&](int e) {
+    const int vc = __builtin_amdgcn_readfirstlane((int)tvc[e >> 2]);
+    return (e & 2) ? vc - kHalf : min(vc, kHalf);
+  };
+  auto load_step = [&](int u, lds_u8* slot) {
+    const int e = entry(u);
+    const int64_t row0 = (int64_t)(e >> 2) * kTile + ((e >> 1) & 1) * kHalf;
+    const char* b = reinterpret_cast<const char*>(kbase + row0 * p.ks);
+    dma16(b, 4 * wave < valid_of(e) ? koff : kskip, slot + wave * 1024);
+  };
+  // One step over the step's vch valid keys (sub-block B only when vch > 32).
+  auto step = [&](const lds_u8* slot, int vch) {
+    const f32x16 sa = sub_scores(slot, fa, w, vch, hi);
+    f32x16 sb;
+    const bool two = vch > 32;
+    if (two) sb = sub_scores(slot, fb, w, vch - 32, hi);
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, two ? fmaxf(sa[e], sb[e]) : sa[e]);
+    const float mraw = half_swap_max(mloc);  // the row's raw max over the step's keys
+    mloc = mraw * c;
+    const float m_new = mloc > w.m_run + kRescaleSlack ? mloc : w.m_run;
+    const float mu = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(w.m_run - mu);
+    w.m_run = m_new;
+    w.mu = mu;
+    if (HEAT == kHeatMax) w.blk = fmaxf(w.blk, mraw);
+    float l4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      l4[e >> 2] += __builtin_amdgcn_exp2f(fmaf(sa[e], c, -mu));
+      if (two) l4[e >> 2] += __builtin_amdgcn_exp2f(fmaf(sb[e], c, -mu));
+    }
+    const float lsum = (l4[0] + l4[1]) + (l4[2] + l4[3]);
+    w.l_run = fmaf(w.l_run, alpha, lsum);
+    if (HEAT == kHeatSum) w.blk = fmaf(w.blk, alpha, lsum);
+  };
+  // At a tile's last step: its log2 statistic per row (log-sum-exp for
+  // 'sum', the bf16-rounded raw max times the scale for 'max', as the
+  // reference's heat rounds scores to bf16 before scaling).
+  auto flush = [&](int j) {
+    float l;
+    if (HEAT == kHeatSum) {
+      const float tot = half_swap_sum(w.blk);
+      l = tot > 0.f ? __log2f(tot) + w.mu : -INFINITY;
+      w.blk = 0.f;
+    } else {
+      l = bf16_to_f32(f32_to_bf16(w.blk)) * c;
+      w.blk = -INFINITY;
+    }
+    if (item_ok && hi == 0) p.part[head * p.part_sh + (int64_t)j * p.part_st + qrow] = l;
+  };
+  auto compute_step = [&](int u, const lds_u8* slot) {
+    const int e = entry(u);
+    const int vch = valid_of(e);
+    if (vch > 0) step(slot, vch);
+    if (e & 1) flush(e >> 2);
+  };
+  lds_u8* K0 = (lds_u8*)ring[0];
+  lds_u8* K1 = (lds_u8*)ring[1];
+  lds_u8* K2 = (lds_u8*)ring[2];
+  lds_u8* K3 = (lds_u8*)ring[3];
+  // The ring: step u in slot u & 3; at the top of step u its own load is
+  // waited for (those of u+1, u+2 may stay in flight), then a bare barrier,
+  // then the slot step u-1 used is refilled with step u+3.
+  auto top = [&](int u) {
+    if (u + 2 < n_steps) VEDA_WAIT_VM(2);
+    else if (u + 1 < n_steps) VEDA_WAIT_VM(1);
+    else VEDA_WAIT_VM(0);
+    __builtin_amdgcn_s_barrier();
+  };
+  if (n_steps > 0) load_step(0, K0);
+  if (n_steps > 1) load_step(1, K1);
+  if (n_steps > 2) load_step(2, K2);
+  for (int u = 0; u < n_steps; u += 4) {
+    top(u);
+    if (u + 3 < n_steps) load_step(u + 3, K3);
+    compute_step(u, K0);
+    if (u + 1 >= n_steps) break;
+    top(u + 1);
+    if (u + 4 < n_steps) load_step(u + 4, K0);
+    compute_step(u + 1, K1);
+    if (u + 2 >= n_steps) break;
+    top(u + 2);
+    if (u + 5 < n_steps) load_step(u + 5, K1);
+    compute_step(u + 2, K2);
+    if (u + 3 >= n_steps) break;
+    top(u + 3);
+    if (u + 6 < n_steps) load_step(u + 6, K2);
+    compute_step(u + 3, K3);
+  }
+  const float l = half_swap_sum(w.l_run);
+  if (item_ok && hi == 0)
+    p.lse[head * p.lse_sh + qrow * p.lse_ss] = l > 0.f ? (w.m_run + __log2f(l)) * kLn2 : -INFINITY;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -1242,8 +1426,9 @@ extern "C" int veda_dense_heat_fwd(const void* q, int64_t q_stride_s, int64_t q_
     if (reduce) hfwd_kernel<kHeatMax, true><<<g, kThreads, 0, s>>>(p);
     else hfwd_kernel<kHeatSum, true><<<g, kThreads, 0, s>>>(p);
   } else {
-    if (reduce) hfwd_kernel<kHeatMax, false><<<g, kThreads, 0, s>>>(p);
-    else hfwd_kernel<kHeatSum, false><<<g, kThreads, 0, s>>>(p);
+    const unsigned gs = (unsigned)(n_heads * ((n_items + kStatItems - 1) / kStatItems));
+    if (reduce) tstats_kernel<kHeatMax><<<gs, kStatThreads, 0, s>>>(p);
+    else tstats_kernel<kHeatSum><<<gs, kStatThreads, 0, s>>>(p);
   }
   return check_launch("veda_dense_heat_fwd");
 }
