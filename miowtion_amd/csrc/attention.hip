@@ -158,8 +158,7 @@ __device__ __forceinline__ HDma hdma_offsets(int64_t ks, int64_t vs, int wave, i
 
 
 // Issues the loads of the step at key row row0 (64 rows, the first vch of
-// them valid) into `slot`. Without PV only K is loaded.
-template <bool PV>
+// them valid) into `slot`.
 __device__ __forceinline__ void issue_step(const uint16_t* kbase, const uint16_t* vbase,
                                            const FwdParams& p, const HDma& d, int64_t row0,
                                            int vch, int wave, int lane, lds_u8* slot) {
@@ -170,7 +169,7 @@ __device__ __forceinline__ void issue_step(const uint16_t* kbase, const uint16_t
     const int seg = 2 * wave + u;
     const bool live = 4 * seg < vch;
     dma16(kb, live ? d.k[u] : d.k_skip[u], slot + seg * 1024);
-    if (PV) dma16(vb, live ? d.v[u] : d.v_skip[u], slot + kHalfBytes + seg * 1024);
+    dma16(vb, live ? d.v[u] : d.v_skip[u], slot + kHalfBytes + seg * 1024);
   }
 }
 
@@ -199,7 +198,7 @@ __device__ __forceinline__ HFrag hfrag_offsets(int kh, int lane) {
 
 // One step for this wave's 32 rows and 32 keys from `slot`; keys at or past
 // vch (of the half) are masked.
-template <int HEAT, bool PV>
+template <int HEAT>
 __device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float c, int vch,
                                       int kh, int hi, WaveState& w) {
   u32x4 kf[8];
@@ -246,7 +245,6 @@ __device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float 
   w.l_run = fmaf(w.l_run, alpha, lsum);
   // heat 'sum': this lane's 16 keys, relative to mu like l
   if (HEAT == kHeatSum) w.blk = fmaf(w.blk, alpha, lsum);
-  if (!PV) return;
   u32x4 pk[2];
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)
@@ -274,15 +272,12 @@ __device__ __forceinline__ void hstep(const lds_u8* slot, const HFrag& f, float 
 
 
 // The teacher's pass: every key tile of a tile layout in order, its padding
-// rows masked, with the block statistic of the heat and, with PV, the
-// dense output.
-template <int HEAT, bool PV>
+// rows masked, with the block statistic of the heat and the dense output.
+template <int HEAT>
 __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
-  // Without PV a slot holds K only, and the steps are 16-bit (tile, half)
-  // entries plus a byte per tile of valid counts: the statistics-only pass
-  // then needs 75 KB of LDS, so two workgroups share a CU and hide each
-  // other's latencies.
-  constexpr int kSlot = PV ? kSlotBytes : kHalfBytes;
+  // The steps are 16-bit (tile, half) entries plus a byte per tile of
+  // valid counts.
+  constexpr int kSlot = kSlotBytes;
   __shared__ __attribute__((aligned(1024))) uint8_t slot0[kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t slot1[kSlot];
   __shared__ __attribute__((aligned(1024))) uint8_t slot2[kSlot];
@@ -377,7 +372,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   // a step with no valid key (an empty tile) loads the tile's first rows,
   // which exist; its keys are all masked
   auto load_step = [&](int u, lds_u8* slot) {
-    issue_step<PV>(kbase, vbase, p, dma, step_row(u), step_vch(u), wave, lane, slot);
+    issue_step(kbase, vbase, p, dma, step_row(u), step_vch(u), wave, lane, slot);
   };
   // Prologue: steps 0, 1, 2 into slots 0, 1, 2.
   if (n_steps > 0) load_step(0, sl0);
@@ -392,9 +387,9 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   // for its own loads, and every fragment read of the previous step has been
   // consumed by an MFMA before its wave reaches the barrier.
   auto wait_step = [&](int u) {
-    // loads per wave per step: 4 (K and V), 2 without PV
-    if (u + 2 < n_steps) VEDA_WAIT_VM(PV ? 8 : 4);
-    else if (u + 1 < n_steps) VEDA_WAIT_VM(PV ? 4 : 2);
+    // loads per wave per step: 4 (K and V)
+    if (u + 2 < n_steps) VEDA_WAIT_VM(8);
+    else if (u + 1 < n_steps) VEDA_WAIT_VM(4);
     else VEDA_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
   };
@@ -442,7 +437,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   auto compute_step = [&](int u, const lds_u8* slot) {
     const int vch = step_vch(u);
     if (HEAT != kNoHeat && kh == 0 && pend_j >= 0) write_pending();
-    if (vch > 32 * kh) hstep<HEAT, PV>(slot, frag, c, vch, kh, hi, w);
+    if (vch > 32 * kh) hstep<HEAT>(slot, frag, c, vch, kh, hi, w);
     if (HEAT != kNoHeat) {
       const int32_t word = step_word(u);
       if (word & kTileEnd) flush_tile((word >> 7 & 0x7FFFFF) / kTile);
@@ -474,7 +469,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   float* red = reinterpret_cast<float*>(qg < 2 ? slot0 : slot1) + (qg & 1) * 64 * 64;
   float* ml = reinterpret_cast<float*>(slot2);  // [qg][m | l][32]
   if (kh == 1) {
-    if (PV) {
+    {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -496,7 +491,7 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
   const float inv = l > 0.f ? 1.f / l : 0.f;
   uint16_t* orow = p.out + qrow * p.os + head * p.oh;
 #pragma unroll
-  for (int dt = 0; dt < (PV ? 4 : 0); ++dt)
+  for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float v4[4];
@@ -1423,8 +1418,8 @@ extern "C" int veda_dense_heat_fwd(const void* q, int64_t q_stride_s, int64_t q_
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const unsigned g = (unsigned)items;
   if (out != nullptr) {
-    if (reduce) hfwd_kernel<kHeatMax, true><<<g, kThreads, 0, s>>>(p);
-    else hfwd_kernel<kHeatSum, true><<<g, kThreads, 0, s>>>(p);
+    if (reduce) hfwd_kernel<kHeatMax><<<g, kThreads, 0, s>>>(p);
+    else hfwd_kernel<kHeatSum><<<g, kThreads, 0, s>>>(p);
   } else {
     const unsigned gs = (unsigned)(n_heads * ((n_items + kStatItems - 1) / kStatItems));
     if (reduce) tstats_kernel<kHeatMax><<<gs, kStatThreads, 0, s>>>(p);
