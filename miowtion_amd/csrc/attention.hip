@@ -534,22 +534,29 @@ struct SDma {
   uint32_t k[4], v[4], k_skip[4], v_skip[4];
 };
 
+// Source offsets of wave `wave`'s four 1 KB segments (rows 16 wave .. + 15
+// of the 64-row slot). Waves 0, 1 fill sub-block a (slot rows 0 .. 31),
+// waves 2, 3 sub-block b (slot rows 32 .. 63); each pair's offsets count
+// from its own sub-block's first source row, so the two sub-blocks of a
+// step may come from different key tiles.
 __device__ __forceinline__ SDma sdma_offsets(int64_t ks, int64_t vs, int wave, int lane) {
   SDma d;
   const int lr = lane >> 4, pc = lane & 15;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int row = 4 * (4 * wave + u) + lr;
+    const int src = row - (wave >= 2 ? 32 : 0);
     const int kc = (pc ^ (row & 15)) << 3, vc = (pc ^ ((row & 3) << 2)) << 3;
-    d.k[u] = (uint32_t)((row * ks + kc) * 2);
-    d.v[u] = (uint32_t)((row * vs + vc) * 2);
+    d.k[u] = (uint32_t)((src * ks + kc) * 2);
+    d.v[u] = (uint32_t)((src * vs + vc) * 2);
     d.k_skip[u] = (uint32_t)((lr * ks + kc) * 2);
     d.v_skip[u] = (uint32_t)((lr * vs + vc) * 2);
   }
   return d;
 }
 
-// Scores of one 32-key sub-block, masked past `lim` keys of it (lim >= 32: none).
+// Scores of one 32-key sub-block, masked past `lim` keys of it (lim >= 32:
+// none; lim <= 0: all).
 __device__ __forceinline__ f32x16 sub_scores(const lds_u8* slot, const HFrag& f,
                                              const WaveState& w, int lim, int hi) {
   u32x4 kf[8];
@@ -594,21 +601,20 @@ __device__ __forceinline__ void pack_probs(const float (&ps)[16], u32x4 (&pk)[2]
     for (int m = 0; m < 4; ++m) pk[kk][m] = pack_bf16x2(ps[8 * kk + 2 * m], ps[8 * kk + 2 * m + 1]);
 }
 
-// One step of one wave over the step's vch valid keys (sub-block B only
-// when vch > 32): the same online softmax as hstep, over 64 keys.
-template <bool TWO>
+// One step of one wave over its two 32-key sub-blocks, la and lb valid keys
+// (as sub_scores' lim): the same online softmax as hstep, over 64 keys.
+// Both sub-blocks are always computed: one code path per step keeps the
+// accumulators in the same registers from step to step (a path that skips
+// sub-block b makes the compiler move O between register sets every step).
 __device__ __forceinline__ void sstep(const lds_u8* slot, const HFrag& fa, const HFrag& fb,
-                                      float c, int vch, int hi, WaveState& w) {
-  const f32x16 sa = sub_scores(slot, fa, w, vch, hi);
-  f32x16 sb;
-  if (TWO) sb = sub_scores(slot, fb, w, vch - 32, hi);
+                                      float c, int la, int lb, int hi, WaveState& w) {
+  const f32x16 sa = sub_scores(slot, fa, w, la, hi);
+  const f32x16 sb = sub_scores(slot, fb, w, lb, hi);
   float mloc = -INFINITY;
 #pragma unroll
   for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sa[e]);
-  if (TWO) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sb[e]);
-  }
+  for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sb[e]);
   mloc = half_swap_max(mloc) * c;
   const float m_new = mloc > w.m_run + kRescaleSlack ? mloc : w.m_run;
   const float mu = m_new == -INFINITY ? 0.f : m_new;
@@ -621,18 +627,15 @@ __device__ __forceinline__ void sstep(const lds_u8* slot, const HFrag& fa, const
 #pragma unroll
   for (int g = 0; g < 4; ++g) l4[g] = (pa[4 * g] + pa[4 * g + 1]) + (pa[4 * g + 2] + pa[4 * g + 3]);
   float lsum = (l4[0] + l4[1]) + (l4[2] + l4[3]);
-  if (TWO) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) pb[e] = __builtin_amdgcn_exp2f(fmaf(sb[e], c, -mu));
+  for (int e = 0; e < 16; ++e) pb[e] = __builtin_amdgcn_exp2f(fmaf(sb[e], c, -mu));
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      l4[g] = (pb[4 * g] + pb[4 * g + 1]) + (pb[4 * g + 2] + pb[4 * g + 3]);
-    lsum += (l4[0] + l4[1]) + (l4[2] + l4[3]);
-  }
+  for (int g = 0; g < 4; ++g) l4[g] = (pb[4 * g] + pb[4 * g + 1]) + (pb[4 * g + 2] + pb[4 * g + 3]);
+  lsum += (l4[0] + l4[1]) + (l4[2] + l4[3]);
   w.l_run = fmaf(w.l_run, alpha, lsum);
   u32x4 ka[2], kb[2];
   pack_probs(pa, ka);
-  if (TWO) pack_probs(pb, kb);
+  pack_probs(pb, kb);
   if (__any(alpha != 1.f)) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
@@ -640,7 +643,7 @@ __device__ __forceinline__ void sstep(const lds_u8* slot, const HFrag& fa, const
       for (int e = 0; e < 16; ++e) w.o[dt][e] *= alpha;
   }
   sub_pv(slot, fa, ka, w);
-  if (TWO) sub_pv(slot, fb, kb, w);
+  sub_pv(slot, fb, kb, w);
 }
 
 // One 32-key sub-block of a compensation step (the virtual keys of key
@@ -750,7 +753,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   __shared__ uint8_t tvc[LISTS ? kMaxBlocks : 1];
   // virtual keys: per key tile, its real row count if dropped, else 0
   __shared__ __attribute__((aligned(16))) uint8_t vwt[VKEYS ? kMaxBlocks + kHalf : 4];
-  __shared__ int32_t step_total;
+  __shared__ int32_t step_total, step_big, step_small;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 31, hi = lane >> 5;
@@ -772,10 +775,14 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   if (!LISTS) {
     if (tid == 0) step_total = DENSE ? (int)((p.used + kHalf - 1) / kHalf) : 0;
   } else {
-    // Step list: full-list tiles as two unmasked halves, then the first
-    // halves of the partial-list tiles, then their second halves (those with
-    // more than 64 valid keys), each in list order (ballot-ranked, so the
-    // summation order is deterministic); valid counts in a byte table.
+    // Step list of 64-key halves (j << 2 | half << 1 | full), valid counts
+    // in a byte table. Halves with more than 32 valid keys take a step each,
+    // from the front of `steps`: the full-list tiles' two halves, then the
+    // partial-list halves in list order. Halves with 1..32 valid keys (the
+    // ragged ends of partial tiles) go to the back of `steps`, downwards,
+    // and are computed two to a step (one per 32-key sub-block), so no
+    // step leaves a sub-block idle. Ranks come from ballots, so the order,
+    // and with it the summation order, is deterministic.
     for (int j = tid; j < nk; j += kThreads2) tvc[j] = (uint8_t)min(max(p.valid_count[j], 0), kTile);
     const int64_t li_ = head * p.n_q_tiles + r;
     const int ld = (int)p.list_ld;
@@ -790,25 +797,42 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       steps[2 * i + 1] = ok ? (uint16_t)((j << 2) | 3) : kVoidStep;
     }
     if (wave == 0) {
-      int h1 = 0;
+      int na = 2 * nf, nb = 0;
       for (int i0 = 0; i0 < np; i0 += 64) {
         const int i = i0 + lane;
         int vc = 0;
         int32_t j = -1;
+        bool ok = false;
         if (i < np) {
           j = pl[i];
-          const bool ok = j >= 0 && j < nk;
+          ok = j >= 0 && j < nk;
           if (ok) vc = min(max(p.valid_count[j], 0), kTile);
-          steps[2 * nf + i] = ok ? (uint16_t)(j << 2) : kVoidStep;
         }
-        const bool two = i < np && vc > kHalf;
-        const uint64_t bal = __ballot(two);
-        const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
-        if (two) steps[2 * nf + np + h1 + rank] = (uint16_t)((j << 2) | 2);
-        h1 += __builtin_popcountll(bal);
+        // an entry outside [0, n_k) or a tile with no valid key: one void
+        // step, as a full-list entry outside [0, n_k) is
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int vch = half ? vc - kHalf : min(vc, kHalf);
+          const bool has = i < np && (half == 0 || vch > 0);
+          const bool big = has && (vch > 32 || vc == 0);
+          const bool small = has && !big;
+          const uint16_t e = ok && vc > 0 ? (uint16_t)((j << 2) | (half << 1)) : kVoidStep;
+          const uint64_t ba = __ballot(big), bs = __ballot(small);
+          const int ra = __builtin_amdgcn_mbcnt_hi((uint32_t)(ba >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)ba, 0));
+          const int rs = __builtin_amdgcn_mbcnt_hi((uint32_t)(bs >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bs, 0));
+          if (big) steps[na + ra] = e;
+          if (small) steps[2 * kMaxBlocks - 1 - (nb + rs)] = e;
+          na += __builtin_popcountll(ba);
+          nb += __builtin_popcountll(bs);
+        }
       }
-      if (lane == 0) step_total = 2 * nf + np + h1;
+      if (lane == 0) {
+        step_total = na + (nb + 1) / 2;
+        step_big = na;
+        step_small = nb;
+      }
     }
   }
 
@@ -835,22 +859,12 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   }
   __syncthreads();  // step list, weights, valid counts and list step count ready
   const int n_lsteps = __builtin_amdgcn_readfirstlane(step_total);
+  const int n_big = LISTS ? __builtin_amdgcn_readfirstlane(step_big) : 0;
+  const int n_small = LISTS ? __builtin_amdgcn_readfirstlane(step_small) : 0;
   const int n_steps = n_lsteps + n_virt;
 
-  // (first key row, valid keys) of step u; steps n_lsteps .. are virtual
-  auto decode = [&](int u, int64_t& row0, int& vch) {
-    if (VKEYS && u >= n_lsteps) {
-      const int v = u - n_lsteps;
-      row0 = (int64_t)v * kHalf;
-      vch = min(nk - v * kHalf, kHalf);
-      return;
-    }
-    if (DENSE) {
-      row0 = (int64_t)u * kHalf;
-      vch = (int)min(p.used - row0, (int64_t)kHalf);
-      return;
-    }
-    const int e = __builtin_amdgcn_readfirstlane(steps[u]);
+  // (first key row, valid keys) of a list half
+  auto half_keys = [&](int e, int64_t& row0, int& vch) {
     if (e == kVoidStep) {
       row0 = 0;
       vch = 0;
@@ -861,6 +875,34 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     row0 = (int64_t)j * kTile + half * kHalf;
     vch = half ? vc - kHalf : min(vc, kHalf);
   };
+  // Step u: sub-block a is key rows row0 .. + 31 with la valid keys,
+  // sub-block b rows rowb .. + 31 with lb (as sub_scores' lim). A 64-key
+  // step has rowb = row0 + 32, lb = la - 32; a step of two ragged halves
+  // takes one each. Steps n_lsteps .. are virtual.
+  auto decode = [&](int u, int64_t& row0, int& la, int64_t& rowb, int& lb) {
+    if (VKEYS && u >= n_lsteps) {
+      const int v = u - n_lsteps;
+      row0 = (int64_t)v * kHalf;
+      la = min(nk - v * kHalf, kHalf);
+    } else if (DENSE) {
+      row0 = (int64_t)u * kHalf;
+      la = (int)min(p.used - row0, (int64_t)kHalf);
+    } else if (u < n_big) {
+      half_keys(__builtin_amdgcn_readfirstlane(steps[u]), row0, la);
+    } else {
+      const int k = 2 * (u - n_big);
+      half_keys(__builtin_amdgcn_readfirstlane(steps[2 * kMaxBlocks - 1 - k]), row0, la);
+      if (k + 1 < n_small) {
+        half_keys(__builtin_amdgcn_readfirstlane(steps[2 * kMaxBlocks - 2 - k]), rowb, lb);
+      } else {
+        rowb = 0;
+        lb = 0;
+      }
+      return;
+    }
+    rowb = row0 + 32;
+    lb = la - 32;
+  };
   const uint16_t* kbase = p.k + head * p.kh;
   const uint16_t* vbase = p.v + head * p.vh;
   const float c = p.scale_log2;
@@ -868,19 +910,21 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   const SDma cdma = sdma_offsets(VKEYS ? p.cs : 0, VKEYS ? p.cs : 0, wave, lane);  // summaries
   const HFrag fa = hfrag_offsets(0, lane), fb = hfrag_offsets(1, lane);
   auto load_step = [&](int u, lds_u8* slot) {
-    int64_t row0;
-    int vch;
-    decode(u, row0, vch);
+    int64_t row0, rowb;
+    int vch, lb;
+    decode(u, row0, vch, rowb, lb);
     if (VKEYS && u >= n_lsteps) {
       // summaries; in the last step rows past n_k do not exist, so every
       // lane reads a row below vch (the extra rows carry weight 0)
       const char* kb = reinterpret_cast<const char*>(p.kc + head * p.ch + row0 * p.cs);
       const char* vb = reinterpret_cast<const char*>(p.vc + head * p.ch + row0 * p.cs);
       if (vch == kHalf) {
+        // cdma's offsets of waves 2, 3 count from row 32
+        const int64_t sb = wave >= 2 ? 32 * p.cs * 2 : 0;
 #pragma unroll
         for (int u4 = 0; u4 < 4; ++u4) {
-          dma16(kb, cdma.k[u4], slot + (4 * wave + u4) * 1024);
-          dma16(vb, cdma.v[u4], slot + kHalfBytes + (4 * wave + u4) * 1024);
+          dma16(kb + sb, cdma.k[u4], slot + (4 * wave + u4) * 1024);
+          dma16(vb + sb, cdma.v[u4], slot + kHalfBytes + (4 * wave + u4) * 1024);
         }
         return;
       }
@@ -895,9 +939,9 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       }
       return;
     }
-    const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
-    const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
     if (DENSE && vch < kHalf) {
+      const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
+      const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
       // the last dense step: rows past `used` may not exist, so every lane
       // reads a row below vch (masked keys)
       const int lr = lane >> 4, pc = lane & 15;
@@ -911,10 +955,18 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       }
       return;
     }
+    // waves 0, 1: sub-block a from row0; waves 2, 3: sub-block b from rowb.
+    // Segments past a sub-block's valid keys reload its first rows (not
+    // read: masked), so every wave issues the same loads.
+    const bool wa = wave < 2;
+    const int64_t base = wa ? row0 : rowb;
+    const int lim = wa ? vch : lb + 32;
+    const char* kb = reinterpret_cast<const char*>(kbase + base * p.ks);
+    const char* vb = reinterpret_cast<const char*>(vbase + base * p.vs);
 #pragma unroll
     for (int u4 = 0; u4 < 4; ++u4) {
       const int seg = 4 * wave + u4;
-      const bool live = 4 * seg < vch;
+      const bool live = 4 * seg < lim;
       dma16(kb, live ? dma.k[u4] : dma.k_skip[u4], slot + seg * 1024);
       dma16(vb, live ? dma.v[u4] : dma.v_skip[u4], slot + kHalfBytes + seg * 1024);
     }
@@ -930,11 +982,10 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     if (u + 1 < n_steps) load_step(u + 1, nxt);
   };
   auto list_step = [&](int u, const lds_u8* cur) {
-    int64_t row0;
-    int vch;
-    decode(u, row0, vch);
-    if (vch > 32) sstep<true>(cur, fa, fb, c, vch, hi, w);
-    else if (vch > 0) sstep<false>(cur, fa, fb, c, vch, hi, w);
+    int64_t row0, rowb;
+    int la, lb;
+    decode(u, row0, la, rowb, lb);
+    sstep(cur, fa, fb, c, la, lb, hi, w);
   };
   auto virtual_step = [&](int u, const lds_u8* cur) {
     // keys past n_k carry weight 0 (the table is padded), so no mask
