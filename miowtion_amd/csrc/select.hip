@@ -5,7 +5,10 @@
 // 64-bit keys (orderable fp32 score << 32 | ~column), lane-strided so every
 // LDS access is conflict-free; each lane caches the best key of its own
 // columns and k_hi rounds of a wave-wide max extract the winners in
-// descending order. Folding the column into the key makes every key
+// descending order. The rounds are a latency chain, so occupancy is what
+// the kernel runs on: the LDS holds only the row's columns (dynamic size,
+// 20 KB per workgroup at 592 columns: 8 workgroups per CU instead of the 2
+// a 2048-column array allows). Folding the column into the key makes every key
 // distinct, so the order is total: higher score first, lower column first on
 // equal scores.
 //
@@ -25,15 +28,37 @@ __device__ __forceinline__ uint32_t orderable(float v) {
 
 constexpr uint32_t kNegInfKey = 0x007fffffu;  // orderable(-inf)
 
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0u, (uint32_t)v, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0u, (uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// Max over the 64 lanes, wave-uniform. Within a 16-lane row: DPP exchanges
+// with lane ^ 1, lane ^ 2, the mirror inside 8 and the mirror inside 16;
+// across rows: a swizzle with lane ^ 16, then v_permlane32_swap with the
+// lane 32 positions away (it leaves {own, partner} in its two results, in
+// the same order for both halves of the key).
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    uint32_t lo = __shfl_xor((uint32_t)v, m, 64);
-    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
-    uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = o > v ? o : v;
+  v = max_u64(v, dpp_u64<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = max_u64(v, dpp_u64<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = max_u64(v, dpp_u64<0x141>(v));  // row_half_mirror
+  v = max_u64(v, dpp_u64<0x140>(v));  // row_mirror
+  {
+    const uint32_t lo = __builtin_amdgcn_ds_swizzle((uint32_t)v, 0x401F);
+    const uint32_t hi = __builtin_amdgcn_ds_swizzle((uint32_t)(v >> 32), 0x401F);
+    v = max_u64(v, ((uint64_t)hi << 32) | lo);
   }
-  return v;
+  const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32),
+                                                   false, false);
+  v = max_u64(((uint64_t)hi[0] << 32) | lo[0], ((uint64_t)hi[1] << 32) | lo[1]);
+  const uint32_t ulo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t uhi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((uint64_t)uhi << 32) | ulo;
 }
 
 constexpr int kMaxCols = 2048;  // columns of one block (FA4's 2048-block cap)
@@ -45,7 +70,7 @@ __global__ void __launch_bounds__(256) select_topk_kernel(
     const int64_t* __restrict__ rows, int k_lo, int k_hi, const uint8_t* __restrict__ extra,
     int64_t n_extra, int64_t* __restrict__ index, uint8_t* __restrict__ keep, int64_t osh,
     int64_t osr, int64_t col0) {
-  __shared__ uint64_t keys[kSelWaves][kMaxCols];
+  extern __shared__ uint64_t keys[];  // [kSelWaves][per_lane * 64]
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int64_t item = (int64_t)blockIdx.x * kSelWaves + wave;
@@ -54,8 +79,8 @@ __global__ void __launch_bounds__(256) select_topk_kernel(
   const int64_t tile_id = rows[r];
   const int64_t diag = tile_id - block_start;  // column of the own tile, if in block
   const float* srow = scores + h * ssh + r * ssr + block_start;
-  uint64_t* kv = keys[wave];
   const int per_lane = (n_cols + 63) / 64;
+  uint64_t* kv = keys + wave * per_lane * 64;
   uint64_t best = 0;
   int best_j = 0;
   for (int j = 0; j < per_lane; ++j) {
@@ -193,7 +218,8 @@ extern "C" int veda_select_topk(const float* scores, int64_t n_heads, int64_t n_
   const int64_t items = n_heads * n_rows;
   if (items == 0) return VEDA_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  select_topk_kernel<<<(unsigned)((items + kSelWaves - 1) / kSelWaves), 256, 0, s>>>(
+  const size_t lds = (size_t)kSelWaves * ((n_cols + 63) / 64) * 64 * sizeof(uint64_t);  // <= 64 KB
+  select_topk_kernel<<<(unsigned)((items + kSelWaves - 1) / kSelWaves), 256, lds, s>>>(
       scores, n_heads, n_rows, s_stride_h, s_stride_r, block_start, (int)n_cols, kv_ok, rows,
       (int)k_lo, (int)k_hi, extra, n_extra, index, keep, o_stride_h, o_stride_r, col0);
   return check_launch("veda_select_topk");
