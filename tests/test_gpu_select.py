@@ -101,3 +101,18 @@ def test_selection_and_lists_at_full_size(name, ratio):
     got = kernels.index_lists(mask, lay)
     for a, b in zip(got, om.index_lists(want_mask, olay)):
         assert torch.equal(a.cpu(), b)
+
+
+def test_select_at_the_largest_column_count():
+    """2048 key tiles (FA4's per-side cap; the top-k kernel's score rows then
+    take its largest LDS size, 4 waves x 2048 columns x 8 bytes = 64 KB), with
+    ties and -inf rows mixed in: bit-exact against the oracle."""
+    spec = ([(0, (32, 62, 120))], 32 * 62 * 120, 32 * 62 * 120, '1x8x16')
+    lay, olay = _layouts(spec)
+    assert lay.n_tiles == 2048
+    g = torch.Generator().manual_seed(21)
+    scores = torch.rand(2, lay.n_video_tiles, lay.n_tiles, generator=g)
+    scores[0, ::7] = torch.randint(0, 3, (scores[0, ::7].shape), generator=g).float()  # ties
+    scores[1, 5] = float('-inf')  # only the forced diagonal survives
+    _run(scores, lay, olay, pm.column_blocks(lay, pm.Budget(ratio=0.1)),
+         om.column_blocks(olay, om.Budget(ratio=0.1)))
