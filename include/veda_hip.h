@@ -176,6 +176,36 @@ int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t q_stride_h,
                           int64_t lse_stride_s, int64_t front_tiles, void* stream);
 
 /*
+ * Block-sparse attention forward with the tile permutation of q and out
+ * fused in: equal to veda_gather_tiles of q (gather_index, padding slots
+ * zero), then veda_block_sparse_fwd, then veda_scatter_tiles of the result
+ * into out (scatter_index, slots with slot_valid 0 not written). Replaces
+ * that sequence inside the reference's SparseStudent._attend
+ * (miowtion/veda/attention.py:760-788: gather_tiles of q,
+ * fa4.block_sparse_attention, scatter_tiles_). q: bf16 [q_rows, seq_heads,
+ * D] in sequence order; out: bf16 [out_rows, seq_heads, D] (the reference's
+ * [S + 1, H, D] buffer, row S taking padding); heads: int64 [n_heads], head
+ * h' of k, v and the lists is head heads[h'] of q and out. gather_index,
+ * scatter_index: int64 [n_q_tiles * 128], slot_valid: int32 [n_q_tiles *
+ * 128]. A slot whose index or head is outside q / out reads zeros and
+ * writes nothing, as in the gather and scatter kernels. k, v, lists,
+ * valid_count, scale and front_tiles as veda_block_sparse_fwd; no LSE.
+ */
+int veda_block_sparse_fwd_seq(const void* q, int64_t q_rows, int64_t seq_heads,
+                              int64_t q_stride_s, int64_t q_stride_h,
+                              const int64_t* gather_index, const int64_t* scatter_index,
+                              const int32_t* slot_valid, const int64_t* heads,
+                              int64_t n_heads, const void* k, int64_t k_stride_s,
+                              int64_t k_stride_h, const void* v, int64_t v_stride_s,
+                              int64_t v_stride_h, int64_t head_dim, int64_t n_q_tiles,
+                              int64_t n_k_tiles, const int32_t* full_cnt,
+                              const int32_t* full_idx, const int32_t* part_cnt,
+                              const int32_t* part_idx, int64_t list_ld,
+                              const int32_t* valid_count, float scale, void* out,
+                              int64_t out_rows, int64_t o_stride_s, int64_t o_stride_h,
+                              int64_t front_tiles, void* stream);
+
+/*
  * Dense attention of rows [0, used) among themselves on packed [S, H, D]
  * rows (the h3 dense path, miowtion/h3/attention.py:28-102): out rows
  * [used, S) are 0 and their lse is 0. lse: fp32 or NULL, element

@@ -31,6 +31,9 @@ SIGNATURES: dict[str, list] = {
     'veda_index_lists': [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     'veda_block_sparse_fwd': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I,
                               _P, _P, _P, _P, _I, _P, _F, _P, _I, _I, _P, _I, _I, _I, _P],
+    'veda_block_sparse_fwd_seq': [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I,
+                                  _I, _I, _I, _P, _P, _P, _P, _I, _P, _F, _P, _I, _I, _I, _I,
+                                  _P],
     'veda_dense_fwd': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _F, _P,
                        _I, _I, _P, _I, _I, _P],
     'veda_block_heat': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I,

@@ -181,11 +181,21 @@ class SparseStudent:
                 heads: torch.Tensor, out: torch.Tensor) -> None:
         pred = self.predictor
         want = pred.second_order_rank
+        cfg = self.clip.config
+        compensated = cfg.zero_order_compensation or cfg.triton_compensation
+        # Without compensation the attention kernel reads q in sequence order
+        # and scatters its rows itself, so q is only pooled, not permuted.
+        q_tiles = None
+        if compensated:
+            q_res = kernels.gather_and_pool(q, tile_layout, heads, second=bool(want))
+            q_tiles, q_res = q_res[0], q_res[1:]
+        else:
+            q_res = kernels.pool_seq(q, tile_layout, heads, second=bool(want))
         if want:
-            q_tiles, feats_q, sq_q, _ = kernels.gather_and_pool(q, tile_layout, heads, second=True)
+            feats_q, sq_q, _ = q_res
             k_tiles, feats_k, _, var_k = kernels.gather_and_pool(k, tile_layout, heads, second=True)
         else:
-            q_tiles, feats_q = kernels.gather_and_pool(q, tile_layout, heads)
+            (feats_q,) = q_res
             k_tiles, feats_k = kernels.gather_and_pool(k, tile_layout, heads)
             sq_q = var_k = None
         v_tiles = kernels.gather_tiles(v, tile_layout, heads)
@@ -200,15 +210,14 @@ class SparseStudent:
                 logits[:, :tile_layout.n_video_tiles], tile_layout, self.clip.blocks(tile_layout))
             block_mask = veda_mask.dense_block_mask(selection, tile_layout)
             lists = kernels.index_lists(block_mask, tile_layout)
-            cfg = self.clip.config
-            if cfg.zero_order_compensation or cfg.triton_compensation:
+            if compensated:
                 # the lists already hold only kv_ok tiles (index_lists applies it)
                 o_tiles = kernels.compensated_attention(q_tiles, k_tiles, v_tiles, block_mask,
                                                         tile_layout, lists)
+                kernels.scatter_tiles_(out, o_tiles, tile_layout, heads)
             else:
-                o_tiles = kernels.block_sparse_attention_lists(q_tiles, k_tiles, v_tiles, lists,
-                                                               tile_layout)
-        kernels.scatter_tiles_(out, o_tiles, tile_layout, heads)
+                kernels.block_sparse_attention_seq_(out, q, k_tiles, v_tiles, lists, tile_layout,
+                                                    heads)
         self.last.setdefault('parts', []).append(
             dict(shape=tile_layout, heads=heads, selection=selection, lists=lists,
                  logits=logits))

@@ -88,6 +88,17 @@ struct FwdParams {
   float* part;
   int64_t part_sh, part_st;
   int64_t front;  // sparse walks: query tiles [n_q - front, n_q) of every head go first
+  // Sparse walk in sequence order (veda_block_sparse_fwd_seq; NULL: tile
+  // order): query slot s reads q row seq_q[s] and writes out row seq_o[s]
+  // of head seq_heads[h'], q being [seq_rows, seq_heads_n, D] and out
+  // [out_rows, seq_heads_n, D]. A slot whose slot_ok is 0, or whose row or
+  // head is out of range, reads zeros and writes nothing (the semantics of
+  // the gather and scatter kernels).
+  const int64_t* seq_q;
+  const int64_t* seq_o;
+  const int32_t* slot_ok;
+  const int64_t* seq_heads;
+  int64_t seq_rows, seq_heads_n, out_rows;
 };
 
 // Block statistic collected for the teacher heat: none, log-sum-exp, max.
@@ -837,11 +848,17 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   }
 
   WaveState w;
+  const uint16_t* qptr = p.q + qrow * p.qs + head * p.qh;
+  bool q_live = !DENSE || qrow < p.used;
+  if (MODE == kSparse && p.seq_q != nullptr) {
+    const int64_t sh = p.seq_heads[head], src = p.seq_q[qrow];
+    q_live = p.slot_ok[qrow] != 0 && src >= 0 && src < p.seq_rows && sh >= 0 &&
+             sh < p.seq_heads_n;
+    qptr = p.q + (q_live ? src : 0) * p.qs + (q_live ? sh : 0) * p.qh;
+  }
 #pragma unroll
   for (int s = 0; s < 8; ++s)
-    w.qf[s] = (!DENSE || qrow < p.used)
-                  ? as_bf16x8(ld16(p.q + qrow * p.qs + head * p.qh + 16 * s + 8 * hi))
-                  : as_bf16x8(u32x4{0, 0, 0, 0});
+    w.qf[s] = q_live ? as_bf16x8(ld16(qptr + 16 * s + 8 * hi)) : as_bf16x8(u32x4{0, 0, 0, 0});
 #pragma unroll
   for (int s = 0; s < 8; ++s) asm volatile("" : : "v"(w.qf[s]));
 #pragma unroll
@@ -1055,6 +1072,13 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   const float inv = MODE == kVirtualOnly ? 1.f / (1.f + l) : (l > 0.f && row_real) ? 1.f / l : 0.f;
   if (DENSE && qrow >= p.q_rows) return;  // rows past seq_len do not exist
   uint16_t* orow = p.out + qrow * p.os + head * p.oh;
+  bool o_live = true;
+  if (MODE == kSparse && p.seq_o != nullptr) {
+    const int64_t sh = p.seq_heads[head], dst = p.seq_o[qrow];
+    o_live = p.slot_ok[qrow] != 0 && dst >= 0 && dst < p.out_rows && sh >= 0 &&
+             sh < p.seq_heads_n;
+    orow = p.out + (o_live ? dst : 0) * p.os + (o_live ? sh : 0) * p.oh;
+  }
   const uint16_t* krow = MODE == kVirtualOnly ? p.o_kept + qrow * p.oks + head * p.okh : nullptr;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -1076,7 +1100,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       for (int m = 0; m < 4; ++m)
         v4[m] = (MODE == kVirtualOnly ? kept4[m] + w.o[dt][e + m] : w.o[dt][e + m]) * inv;
       uint32_t w0 = pack_bf16x2(v4[0], v4[1]), w1 = pack_bf16x2(v4[2], v4[3]);
-      *reinterpret_cast<u32x2*>(orow + d) = u32x2{w0, w1};
+      if (o_live) *reinterpret_cast<u32x2*>(orow + d) = u32x2{w0, w1};
     }
   if ((MODE == kSparse || DENSE) && p.lse != nullptr && hi == 0)
     p.lse[head * p.lse_sh + qrow * p.lse_ss] =
@@ -1321,6 +1345,67 @@ extern "C" int veda_block_sparse_fwd(const void* q, int64_t q_stride_s, int64_t 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   sfwd_kernel<kSparse><<<(unsigned)items, kThreads2, 0, s>>>(p);
   return check_launch("veda_block_sparse_fwd");
+}
+
+extern "C" int veda_block_sparse_fwd_seq(
+    const void* q, int64_t q_rows, int64_t seq_heads, int64_t q_stride_s, int64_t q_stride_h,
+    const int64_t* gather_index, const int64_t* scatter_index, const int32_t* slot_valid,
+    const int64_t* heads, int64_t n_heads, const void* k, int64_t k_stride_s, int64_t k_stride_h,
+    const void* v, int64_t v_stride_s, int64_t v_stride_h, int64_t head_dim, int64_t n_q_tiles,
+    int64_t n_k_tiles, const int32_t* full_cnt, const int32_t* full_idx, const int32_t* part_cnt,
+    const int32_t* part_idx, int64_t list_ld, const int32_t* valid_count, float scale, void* out,
+    int64_t out_rows, int64_t o_stride_s, int64_t o_stride_h, int64_t front_tiles, void* stream) {
+  VEDA_REQUIRE(head_dim == kD, "block_sparse_fwd_seq: head_dim must be 128, got %lld",
+               (long long)head_dim);
+  VEDA_REQUIRE(front_tiles >= 0 && front_tiles <= n_q_tiles,
+               "block_sparse_fwd_seq: front_tiles %lld outside [0, n_q_tiles]",
+               (long long)front_tiles);
+  VEDA_REQUIRE(n_heads >= 0 && n_q_tiles >= 0 && n_k_tiles >= 0 && q_rows >= 0 && out_rows >= 0 &&
+                   seq_heads >= 0,
+               "block_sparse_fwd_seq: negative size");
+  VEDA_REQUIRE(list_ld >= n_k_tiles, "block_sparse_fwd_seq: list_ld %lld < n_k_tiles %lld",
+               (long long)list_ld, (long long)n_k_tiles);
+  VEDA_REQUIRE(gather_index != nullptr && scatter_index != nullptr && slot_valid != nullptr &&
+                   heads != nullptr,
+               "block_sparse_fwd_seq: the gather / scatter indices, slot_valid and heads are required");
+  VEDA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) &&
+                   q_stride_s % 8 == 0 && q_stride_h % 8 == 0 && k_stride_s % 8 == 0 &&
+                   k_stride_h % 8 == 0 && v_stride_s % 8 == 0 && v_stride_h % 8 == 0 &&
+                   o_stride_s % 4 == 0 && o_stride_h % 4 == 0,
+               "block_sparse_fwd_seq: rows must be 16-byte aligned");
+  const int64_t items = n_heads * n_q_tiles;
+  if (items == 0) return VEDA_OK;
+  VEDA_REQUIRE(n_k_tiles >= 1 && n_k_tiles <= kMaxBlocks,
+               "block_sparse_fwd_seq: n_k_tiles %lld outside [1, %d]", (long long)n_k_tiles,
+               kMaxBlocks);
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.qs = q_stride_s; p.qh = q_stride_h;
+  p.ks = k_stride_s; p.kh = k_stride_h;
+  p.vs = v_stride_s; p.vh = v_stride_h;
+  p.n_heads = n_heads; p.n_q_tiles = n_q_tiles; p.n_k_tiles = n_k_tiles;
+  p.full_cnt = full_cnt; p.full_idx = full_idx;
+  p.part_cnt = part_cnt; p.part_idx = part_idx;
+  p.list_ld = list_ld;
+  p.valid_count = valid_count;
+  p.q_rows = n_q_tiles * kTile;
+  p.scale_log2 = (float)((double)scale * 1.4426950408889634);
+  p.out = static_cast<uint16_t*>(out);
+  p.os = o_stride_s; p.oh = o_stride_h;
+  p.lse = nullptr;
+  p.front = front_tiles;
+  p.seq_q = gather_index;
+  p.seq_o = scatter_index;
+  p.slot_ok = slot_valid;
+  p.seq_heads = heads;
+  p.seq_rows = q_rows;
+  p.seq_heads_n = seq_heads;
+  p.out_rows = out_rows;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  sfwd_kernel<kSparse><<<(unsigned)items, kThreads2, 0, s>>>(p);
+  return check_launch("veda_block_sparse_fwd_seq");
 }
 
 extern "C" int veda_compensated_attention(

@@ -62,6 +62,15 @@ def gather_and_pool(x: torch.Tensor, layout: tiling.TileLayout,
     return tuple(res)
 
 
+def pool_seq(x: torch.Tensor, layout: tiling.TileLayout, heads: torch.Tensor | None,
+             second: bool = False) -> tuple:
+    """The pooling of gather_and_pool without writing the tile-ordered rows
+    (one read of x): (feats,) or (feats, E[x^2], Var(x))."""
+    res = ops.gather(x, layout.gather_index, layout.slot_valid, layout.valid_count,
+                     _heads(x, heads), False, True, second)
+    return tuple(res[1:])
+
+
 def pool_tiles(x: torch.Tensor, layout: tiling.TileLayout, second: str | None = None) -> torch.Tensor:
     """Pooling of already tile-ordered rows [N, H', D] (predictor.py:82-130):
     [H', n, 3D] fp32 [mean | max | min], or [H', n, D] E[x^2] ('raw') /
@@ -198,6 +207,20 @@ def block_sparse_attention_lists(q, k, v, lists, layout: tiling.TileLayout,
                                layout.valid_count, return_lse,
                                _front_tiles(layout, q.shape[0] // 128))
     return (res[0], res[1]) if return_lse else res[0]
+
+
+def block_sparse_attention_seq_(out: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
+                                v: torch.Tensor, lists, layout: tiling.TileLayout,
+                                heads: torch.Tensor | None) -> None:
+    """scatter_tiles_(out, block_sparse_attention_lists(gather_tiles(q), k, v,
+    lists), layout, heads) in one kernel: q [S, H, D] in sequence order,
+    out the [S + 1, H, D] scatter buffer, k / v tile-ordered [N, H', D]
+    (the sequence of miowtion/veda/attention.py:760-788)."""
+    part_cnt, part_idx, full_cnt, full_idx = lists
+    ops.block_sparse_fwd_seq_(out, q, k, v, layout.gather_index, layout.scatter_index,
+                              layout.slot_valid, _heads(q, heads), part_cnt, part_idx, full_cnt,
+                              full_idx, layout.valid_count,
+                              _front_tiles(layout, layout.gather_index.numel() // 128))
 
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, used: int,

@@ -264,6 +264,49 @@ def _(q, k, v, part_cnt, part_idx, full_cnt, full_idx, valid_count, return_lse, 
     return [out]
 
 
+@torch.library.custom_op('veda::block_sparse_fwd_seq_', mutates_args=('out',))
+def block_sparse_fwd_seq_(out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          gather_index: torch.Tensor, scatter_index: torch.Tensor,
+                          slot_valid: torch.Tensor, heads: torch.Tensor, part_cnt: torch.Tensor,
+                          part_idx: torch.Tensor, full_cnt: torch.Tensor, full_idx: torch.Tensor,
+                          valid_count: torch.Tensor, front_tiles: int = 0) -> None:
+    """block_sparse_fwd with the permutation of q and out fused in: q [S, H,
+    D] in sequence order is read through gather_index, and out [S + 1, H, D]
+    receives the rows through scatter_index (what gather, block_sparse_fwd
+    and scatter_ do in sequence). heads maps the H' heads of k / v / lists
+    to heads of q and out."""
+    _require_gpu(out, q, k, v, gather_index, scatter_index, slot_valid, heads, part_cnt,
+                 part_idx, full_cnt, full_idx, valid_count)
+    for name, t in (('out', out), ('q', q), ('k', k), ('v', v)):
+        _check_rows(name, t)
+    if q.shape[-1] != 128 or out.shape[1:] != q.shape[1:] or out.dtype != q.dtype:
+        raise ValueError(f'q {tuple(q.shape)} and out {tuple(out.shape)} must be [*, H, 128] alike')
+    n_slots = gather_index.numel()
+    hp = heads.numel()
+    if (n_slots % TILE or scatter_index.numel() != n_slots or slot_valid.numel() != n_slots
+            or gather_index.dtype != torch.int64 or scatter_index.dtype != torch.int64
+            or slot_valid.dtype != torch.int32 or heads.dtype != torch.int64):
+        raise ValueError('gather_index / scatter_index int64 and slot_valid int32 of n_tiles * 128 '
+                         'slots, heads int64')
+    if k.shape != v.shape or k.shape[0] % TILE or k.shape[1] != hp or k.shape[2] != q.shape[2]:
+        raise ValueError(f'k {tuple(k.shape)} / v {tuple(v.shape)} must be [n_k * 128, {hp}, 128]')
+    r_tiles, n_k = n_slots // TILE, k.shape[0] // TILE
+    _check_lists('part', part_cnt, part_idx, hp, r_tiles, n_k)
+    _check_lists('full', full_cnt, full_idx, hp, r_tiles, n_k)
+    if part_idx.shape[3] != full_idx.shape[3]:
+        raise ValueError('part and full lists must have the same row length')
+    if valid_count.numel() < n_k or valid_count.dtype != torch.int32:
+        raise ValueError('valid_count must be int32 [n_k_tiles]')
+    _native.call('veda_block_sparse_fwd_seq', q.data_ptr(), q.shape[0], q.shape[1], q.stride(0),
+                 q.stride(1), gather_index.data_ptr(), scatter_index.data_ptr(),
+                 slot_valid.data_ptr(), heads.data_ptr(), hp, k.data_ptr(), k.stride(0),
+                 k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), q.shape[2], r_tiles, n_k,
+                 full_cnt.data_ptr(), full_idx.data_ptr(), part_cnt.data_ptr(),
+                 part_idx.data_ptr(), part_idx.shape[3], valid_count.data_ptr(),
+                 1.0 / math.sqrt(q.shape[2]), out.data_ptr(), out.shape[0], out.stride(0),
+                 out.stride(1), front_tiles, _stream(q))
+
+
 def _check_lists(name: str, cnt: torch.Tensor, idx: torch.Tensor, heads: int, rows: int,
                  cols: int) -> None:
     if (idx.dtype != torch.int32 or idx.dim() != 4 or tuple(idx.shape[:3]) != (1, heads, rows)

@@ -208,3 +208,30 @@ def test_largest_tile_count():
     with pytest.raises(ValueError, match='n_k_tiles'):
         ops.block_sparse_fwd(qt[:128].cuda(), kv, kv, cnt, idx, cnt, idx,
                              torch.full((2049,), 128, dtype=torch.int32, device='cuda'), False)
+
+
+@pytest.mark.parametrize('name', ['small', 'C3b'])
+def test_sequence_order_entry_equals_gather_attend_scatter(name):
+    """veda_block_sparse_fwd_seq (q read through the gather index, rows
+    written through the scatter index) against gather -> sparse forward ->
+    scatter on the same inputs: bit-identical buffers, padding rows and the
+    heads outside the subset untouched. The subset is heads 1 and 3 of 4."""
+    spec = helpers.small_layout() if name == 'small' else helpers.CONFIGS[name]
+    lay = helpers.product_layout(*spec, device='cuda')
+    q, k, v = (t.cuda() for t in helpers.qkv(lay.seq_len, 4, 128, seed=5))
+    heads = torch.tensor([1, 3], device='cuda')
+    kt, vt = (kernels.gather_tiles(t, lay, heads) for t in (k, v))
+    g = torch.Generator().manual_seed(6)
+    mask = (torch.rand(2, lay.n_tiles, lay.n_tiles, generator=g) < 0.2) | torch.eye(
+        lay.n_tiles, dtype=torch.bool)[None]
+    lists = kernels.index_lists(mask.cuda(), lay)
+    init = torch.randn(lay.seq_len + 1, 4, 128, generator=g).to(torch.bfloat16).cuda()
+    want = init.clone()
+    o_tiles = kernels.block_sparse_attention_lists(kernels.gather_tiles(q, lay, heads), kt, vt,
+                                                   lists, lay)
+    kernels.scatter_tiles_(want, o_tiles, lay, heads)
+    got = init.clone()
+    kernels.block_sparse_attention_seq_(got, q, kt, vt, lists, lay, heads)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), want.cpu())
+    assert torch.equal(got[:, [0, 2]].cpu(), init[:, [0, 2]].cpu())
