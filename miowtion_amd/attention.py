@@ -166,9 +166,18 @@ class SparseStudent:
             return kernels.dense_attention(q, k, v, used)[0]
         self.calls['sparse'] += 1
         seq_len = q.shape[0]
-        out = q.new_zeros(seq_len + 1, *q.shape[1:])
+        groups = self.plan.head_groups(layer_index, self.clip.device)
+        # The reference zero-fills the [S + 1, H, D] buffer (attention.py:732).
+        # When the plan's groups hold every head, every (real row, head) is
+        # written below (each real row is one valid slot of every layout), so
+        # only rows [used, S] need the zeros; the result is the same.
+        out = q.new_empty(seq_len + 1, *q.shape[1:])
+        if sum(g.heads.numel() for g in groups) == q.shape[1]:
+            out[used:].zero_()
+        else:
+            out.zero_()
         self.last = {}
-        for group in self.plan.head_groups(layer_index, self.clip.device):
+        for group in groups:
             tile_layout = self.clip.get(group.shape)
             for heads in group.heads.split(_chunk_heads(tile_layout, self.clip.config.collect_bytes)):
                 self._attend(q, k, v, layer_index, tile_layout, heads, out)

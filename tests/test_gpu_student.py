@@ -91,7 +91,12 @@ def test_sparse_student_dynamic_shapes_and_round_trip():
     student = pa.SparseStudent(clip, plan, pred)
     q, k, v = helpers.qkv(seq_len, H, 128, seed=9)
     q[used:] = 0
-    out = student(q.cuda(), k.cuda(), v.cuda(), 0).cpu()
+    qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+    # a NaN block of the output buffer's size, freed at once: the student's
+    # buffer (allocated uninitialised, only rows past `used` zeroed) reuses
+    # it, so a (row, head) the layer failed to write would show as NaN
+    torch.full((seq_len + 1, H, 128), float('nan'), dtype=torch.bfloat16, device='cuda')
+    out = student(qc, kc, vc, 0).cpu()
     assert (out[used:] == 0).all()
     want = torch.zeros(seq_len, H, 128, dtype=torch.bfloat16)
     for part in student.last['parts']:
