@@ -171,7 +171,7 @@ class SparseStudent:
         # When the plan's groups hold every head, every (real row, head) is
         # written below (each real row is one valid slot of every layout), so
         # only rows [used, S] need the zeros; the result is the same.
-        out = q.new_empty(seq_len + 1, *q.shape[1:])
+        out = self._output_buffer(q, seq_len + 1)
         if sum(g.heads.numel() for g in groups) == q.shape[1]:
             out[used:].zero_()
         else:
@@ -185,6 +185,11 @@ class SparseStudent:
         if used < seq_len:
             out[used:] = 0
         return out
+
+    def _output_buffer(self, q: torch.Tensor, rows: int) -> torch.Tensor:
+        """The [rows, H, D] scatter buffer, uninitialised (every row the
+        layer does not write is zeroed by the caller)."""
+        return q.new_empty(rows, *q.shape[1:])
 
     def _attend(self, q, k, v, layer_index: int, tile_layout: tiling.TileLayout,
                 heads: torch.Tensor, out: torch.Tensor) -> None:

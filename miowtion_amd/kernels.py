@@ -26,15 +26,42 @@ SECOND_RAW = 'raw'
 SECOND_CENTRAL = 'central'
 
 
-def supports(x: torch.Tensor) -> bool:
-    """The kernels can take this tensor (tile_gather_triton.py:55-66)."""
+SUPPORTED_ARCH = 'gfx950'
+# head_dim each family of kernels takes: the permutation and pooling kernels
+# are written for 64 and 128 (tile_gather_triton.py:55-66), the attention,
+# heat and compensation kernels for 128 only.
+_HEAD_DIMS = {'gather': (64, 128), 'attention': (128,), 'heat': (128,)}
+
+
+def _device_arch(device: torch.device) -> str:
+    return torch.cuda.get_device_properties(device).gcnArchName.split(':')[0]
+
+
+def supports(x: torch.Tensor, op: str = 'gather') -> bool:
+    """Whether the kernels of `op` ('gather' for gather / pool / scatter,
+    'attention' for the sparse and dense forwards, their backward and the
+    compensation, 'heat' for the block heat) can take this tensor: the
+    library loads, x is a bf16 tensor with a unit last stride and a head_dim
+    that family implements, on a gfx950 device. The routing predicate of
+    tile_gather_triton.py:55-66: a caller with another path falls through to
+    it when this answers False, instead of reaching a kernel that raises.
+
+    Raises:
+        ValueError: If op is not one of the families above.
+    """
+    if op not in _HEAD_DIMS:
+        raise ValueError(f'op must be one of {sorted(_HEAD_DIMS)}: {op!r}')
+    if not (x.is_cuda and x.dtype == torch.bfloat16 and x.dim() >= 1
+            and x.shape[-1] in _HEAD_DIMS[op] and x.stride(-1) == 1):
+        return False
+    if _device_arch(x.device) != SUPPORTED_ARCH:
+        return False
     from miowtion_amd import _native
     try:
         _native.load()
     except ImportError:
         return False
-    return (x.is_cuda and x.dtype == torch.bfloat16 and x.shape[-1] in (64, 128)
-            and x.stride(-1) == 1)
+    return True
 
 
 def _heads(x: torch.Tensor, heads: torch.Tensor | None) -> torch.Tensor:
@@ -77,7 +104,7 @@ def pool_tiles(x: torch.Tensor, layout: tiling.TileLayout, second: str | None = 
     centred Var(x) ('central')."""
     if second not in (None, SECOND_RAW, SECOND_CENTRAL):
         raise ValueError(f'unknown second moment {second!r}')
-    ident = _identity(layout, x.device)
+    ident = _identity(layout)
     res = ops.gather(x, ident, layout.slot_valid, layout.valid_count,
                      torch.arange(x.shape[1], device=x.device), False, True, second is not None)
     if second is None:
@@ -85,14 +112,13 @@ def pool_tiles(x: torch.Tensor, layout: tiling.TileLayout, second: str | None = 
     return res[2] if second == SECOND_RAW else res[3]
 
 
-_IDENT: dict = {}
-
-
-def _identity(layout: tiling.TileLayout, device) -> torch.Tensor:
-    key = (layout.num_slots, str(device))
-    if key not in _IDENT:
-        _IDENT[key] = torch.arange(layout.num_slots, device=device)
-    return _IDENT[key]
+def _identity(layout: tiling.TileLayout) -> torch.Tensor:
+    """arange(num_slots) on the layout's device, kept on the layout."""
+    hit = layout.derived.get('identity')
+    if hit is None:
+        hit = torch.arange(layout.num_slots, device=layout.valid_count.device)
+        layout.derived['identity'] = hit
+    return hit
 
 
 def scatter_tiles_(out: torch.Tensor, tiled: torch.Tensor, layout: tiling.TileLayout,

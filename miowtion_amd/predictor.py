@@ -145,14 +145,11 @@ class TileScorePredictor:
         return self.layers[layer](feats_q, feats_k, heads, **extra)
 
 
-_LOG_COUNT: dict = {}
-
-
 def log_count(layout: tiling.TileLayout) -> torch.Tensor:
-    """log(max(valid_count, 1)) per key tile, cached per layout."""
-    key = id(layout)
-    hit = _LOG_COUNT.get(key)
-    if hit is None or hit[0] is not layout:
-        hit = (layout, torch.log(layout.valid_count.clamp(min=1).to(torch.float32)))
-        _LOG_COUNT[key] = hit
-    return hit[1]
+    """log(max(valid_count, 1)) per key tile, kept on the layout (so it
+    lives exactly as long as the layout does)."""
+    hit = layout.derived.get('log_count')
+    if hit is None:
+        hit = torch.log(layout.valid_count.clamp(min=1).to(torch.float32))
+        layout.derived['log_count'] = hit
+    return hit

@@ -145,6 +145,9 @@ class TileLayout:
     kv_ok: torch.Tensor
     full_tile: torch.Tensor
     slot_valid: torch.Tensor
+    # Small tensors derived from the layout (per-tile log counts, an
+    # identity index), built on first use and dropped with the layout.
+    derived: dict = dataclasses.field(default_factory=dict, repr=False, compare=False)
 
     @property
     def n_tiles(self) -> int:

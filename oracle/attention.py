@@ -117,21 +117,30 @@ def block_sparse_attention_grads_by_tile(q, k, v, block_mask, valid_count, dout,
     return tuple(grads)
 
 
-def dense_attention(q, k, v, used: int, return_lse=False, q_chunk: int = 1024):
+def dense_attention(q, k, v, used: int, return_lse=False, q_chunk: int = 1024, rows=None):
     """h3/attention.py 'math' backend: rows [0, used) attend among themselves;
-    out zero and lse 0 on padding rows. q/k/v [S, H, D]; lse [S, H]."""
+    out zero and lse 0 on padding rows. q/k/v [S, H, D]; lse [S, H].
+
+    rows: optional 1-D index of the query rows to compute (the sampled
+    checks at BASELINE sizes); out / lse then hold only those rows, in that
+    order, a row at or past `used` giving 0 as a padding row does. Rows are
+    independent, so a sample has the same values as the full call."""
     S, H, D = q.shape
     scale = 1.0 / math.sqrt(D)
-    out = torch.zeros(S, H, D, dtype=torch.float32)
-    lse = torch.zeros(S, H, dtype=torch.float32)
+    if rows is None:
+        rows = torch.arange(S)
+    rows = torch.as_tensor(rows, dtype=torch.int64)
+    out = torch.zeros(rows.numel(), H, D, dtype=torch.float32)
+    lse = torch.zeros(rows.numel(), H, dtype=torch.float32)
+    real = torch.nonzero(rows < used).flatten()
     kf, vf = k[:used].float(), v[:used].float()
     for h in range(H):
-        for q0 in range(0, used, q_chunk):
-            q1 = min(q0 + q_chunk, used)
-            s = (q[q0:q1, h].float() @ kf[:, h].T) * scale
+        for c0 in range(0, real.numel(), q_chunk):
+            pos = real[c0:c0 + q_chunk]
+            s = (q[rows[pos], h].float() @ kf[:, h].T) * scale
             l = torch.logsumexp(s, -1)
-            out[q0:q1, h] = torch.exp(s - l[:, None]) @ vf[:, h]
-            lse[q0:q1, h] = l
+            out[pos, h] = torch.exp(s - l[:, None]) @ vf[:, h]
+            lse[pos, h] = l
     o = out.to(q.dtype)
     return (o, lse) if return_lse else (o, None)
 

@@ -166,6 +166,34 @@ def test_predictor_logits_match_oracle(fp8, second, count):
     assert torch.equal(sel.index.cpu(), idx) and torch.equal(sel.keep.cpu(), keep)
 
 
+def test_predictor_exact_warm_start_gives_the_diagonal_cumulant():
+    """The reference identity (tests/unit/test_veda_predictor_mask.py:240)
+    on the kernels: zero base projections and so_q = so_k = I sqrt(1 / 2D)
+    (1/16 at D = 128, exact in bf16) give mean_q . mean_k / sqrt(D) +
+    E[q^2] . Var(k) / (2D); plus the count term at gain 1 adds log B_j
+    (:325)."""
+    spec = helpers.small_layout()
+    lay = helpers.product_layout(*spec, device='cuda')
+    olay = helpers.oracle_layout(*spec)
+    q, k = helpers.qkv(lay.seq_len, 4, 128, seed=21, n=2)
+    heads = torch.tensor([3, 0])
+    D = 128
+    zero = pp.ProjWeight(torch.zeros(4, 3 * D, D, dtype=torch.bfloat16, device='cuda'))
+    eye = pp.ProjWeight((torch.eye(D) * math.sqrt(0.5 / D)).expand(4, D, D).to(torch.bfloat16)
+                        .contiguous().cuda())
+    pred = pp.LayerPredictor(zero, zero, eye, eye, torch.ones(4, device='cuda'))
+    _, fq, sq, _ = kernels.gather_and_pool(q.cuda(), lay, heads.cuda(), second=True)
+    _, fk, _, vk = kernels.gather_and_pool(k.cuda(), lay, heads.cuda(), second=True)
+    got = pred(fq, fk, heads.cuda(), sq_q=sq, var_k=vk, log_count=pp.log_count(lay)).cpu()
+    oq, ok = ot.gather_tiles(q, olay, heads), ot.gather_tiles(k, olay, heads)
+    mq, mk = op.pool_tiles(oq, olay)[..., :D], op.pool_tiles(ok, olay)[..., :D]
+    want = (mq @ mk.transpose(1, 2) / math.sqrt(D)
+            + op.pool_tiles(oq, olay, 'raw') @ op.pool_tiles(ok, olay, 'central').transpose(1, 2)
+            / (2 * D)
+            + torch.log(olay.valid_count.clamp(min=1).float())[None, None, :])
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-5)
+
+
 @pytest.mark.parametrize('contiguous', [False, True])
 def test_config4_predictor_and_selection_at_config2_geometry(contiguous):
     """BASELINE config 4 at config-2 size: 57,720 tokens, (1,8,16) tiles (592

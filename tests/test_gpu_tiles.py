@@ -98,3 +98,18 @@ def test_round_trip_bit_exact_at_full_size(name):
     kernels.scatter_tiles_(out2, t2, lay, sub)
     assert torch.equal(out2[:seq_len, sub], x[:, sub])
     assert (out2[:seq_len, 0] == 0).all()
+
+
+def test_supports_is_op_specific():
+    """The routing predicate answers per kernel family: d64 only for the
+    permutation kernels, d128 bf16 for all, on the gfx950 device."""
+    from miowtion_amd import kernels
+    assert kernels._device_arch(torch.device('cuda')) == 'gfx950'
+    d128 = torch.zeros(256, 2, 128, dtype=torch.bfloat16, device='cuda')
+    d64 = torch.zeros(256, 2, 64, dtype=torch.bfloat16, device='cuda')
+    for op in ('gather', 'attention', 'heat'):
+        assert kernels.supports(d128, op)
+        assert not kernels.supports(d128.half(), op)
+        assert not kernels.supports(d128.transpose(0, 2), op)
+    assert kernels.supports(d64, 'gather')
+    assert not kernels.supports(d64, 'attention') and not kernels.supports(d64, 'heat')

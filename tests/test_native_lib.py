@@ -92,3 +92,13 @@ def test_host_side_argument_checks():
     with pytest.raises(ValueError, match='reduce'):
         _native.call('veda_heat_combine', None, None, 0, 0, None, None, 1, 1, 1, 5, None, None)
     assert isinstance(lib.veda_last_error(), bytes)
+
+
+def test_supports_refuses_cpu_tensors_and_unknown_ops():
+    import torch
+    from miowtion_amd import kernels
+    x = torch.zeros(4, 2, 128, dtype=torch.bfloat16)
+    for op in ('gather', 'attention', 'heat'):
+        assert not kernels.supports(x, op)
+    with pytest.raises(ValueError, match='op must be'):
+        kernels.supports(x, 'dense')

@@ -90,6 +90,61 @@ def test_count_and_second_order_terms_by_loops():
                 assert abs(float(got[hp, i, j] - want)) < 1e-3 * (1 + abs(float(want)))
 
 
+def test_count_term_adds_exactly_log_b_at_init():
+    """The reference's identity (tests/unit/test_veda_predictor_mask.py:325):
+    with the gain at its initial 1 the count term adds log B_j of the KEY
+    tile j to every row, nothing else (a term indexed by the query tile, or
+    a dropped gain, fails)."""
+    lay = _layout()
+    assert len(set(lay.valid_count.tolist())) > 2        # counts differ per tile
+    g = torch.Generator().manual_seed(8)
+    D = 16
+    q = torch.randn(lay.seq_len, 4, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(lay.seq_len, 4, D, generator=g).to(torch.bfloat16)
+    heads = torch.tensor([0, 2])
+    fq = op.pool_tiles(ot.gather_tiles(q, lay, heads), lay)
+    fk = op.pool_tiles(ot.gather_tiles(k, lay, heads), lay)
+    pq, pk = (torch.randn(4, 3 * D, D, generator=g) * 1e-2 for _ in range(2))
+    plain = op.logits(fq, fk, pq, pk, heads)
+    lc = torch.log(lay.valid_count.clamp(min=1).float())
+    counted = op.logits(fq, fk, pq, pk, heads, gain=torch.ones(4), log_count=lc)
+    delta = counted - plain
+    torch.testing.assert_close(delta, lc.expand_as(delta), rtol=1e-5, atol=1e-5)
+
+
+def test_exact_warm_start_equals_the_diagonal_cumulant():
+    """The reference's identity (tests/unit/test_veda_predictor_mask.py:240):
+    with the base projections zero and the full-rank second-order head at
+    its exact warm start (so_q = so_k = I sqrt(1 / 2D), predictor.py:232-249)
+    the logits are mean_q . mean_k / sqrt(D) + E[q^2] . Var(k) / (2D), with
+    the tile statistics taken here by per-tile loops over the real rows."""
+    lay = _layout()
+    g = torch.Generator().manual_seed(9)
+    D = 16
+    q = torch.randn(lay.seq_len, 4, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(lay.seq_len, 4, D, generator=g).to(torch.bfloat16)
+    heads = torch.tensor([1, 3])
+    qt, kt = ot.gather_tiles(q, lay, heads), ot.gather_tiles(k, lay, heads)
+    zero = torch.zeros(4, 3 * D, D)
+    eye = torch.eye(D).expand(4, D, D) * math.sqrt(0.5 / D)
+    got = op.logits(op.pool_tiles(qt, lay), op.pool_tiles(kt, lay), zero, zero, heads,
+                    sq_q=op.pool_tiles(qt, lay, 'raw'), var_k=op.pool_tiles(kt, lay, 'central'),
+                    so_q=eye, so_k=eye)
+    n = lay.n_tiles
+    mq, mk, sq, vk = (torch.zeros(2, n, D) for _ in range(4))
+    for j in range(n):
+        c = int(lay.valid_count[j])
+        if not c:
+            continue
+        rq = qt.view(n, 128, 2, D)[j, :c].float()
+        rk = kt.view(n, 128, 2, D)[j, :c].float()
+        mq[:, j], mk[:, j] = rq.mean(0), rk.mean(0)
+        sq[:, j] = (rq * rq).mean(0)
+        vk[:, j] = ((rk - rk.mean(0)) ** 2).mean(0)
+    want = mq @ mk.transpose(1, 2) / math.sqrt(D) + sq @ vk.transpose(1, 2) / (2 * D)
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-5)
+
+
 def test_fp8_per_head_quantisation():
     # bundle.py:71-93: per-head amax maps to 448, values round-trip within e4m3
     g = torch.Generator().manual_seed(5)
@@ -162,6 +217,12 @@ def test_dense_attention_matches_sdpa_and_zero_padding():
     assert (out[used:] == 0).all() and (lse[used:] == 0).all()
     s = torch.einsum('qhd,khd->hqk', q[:used].float(), k[:used].float()) / math.sqrt(D)
     torch.testing.assert_close(lse[:used], torch.logsumexp(s, -1).T)
+    # a sample of rows (the form the BASELINE-size GPU checks use): the same
+    # values as the full call, padding rows 0, in the order asked
+    rows = torch.tensor([269, 0, 280, 131, 299, 1])
+    o_s, l_s = oa.dense_attention(q, k, v, used, return_lse=True, q_chunk=4, rows=rows)
+    assert torch.equal(o_s, out[rows]) and torch.equal(l_s, lse[rows])
+    assert (o_s[[2, 4]] == 0).all() and (l_s[[2, 4]] == 0).all()
 
 
 @pytest.mark.parametrize('reduce', ['max', 'sum'])
