@@ -388,6 +388,36 @@ int veda_block_sparse_bwd(const void* q, int64_t q_stride_s, int64_t q_stride_h,
                           int64_t workspace_bytes, int64_t front_tiles, void* stream);
 
 /*
+ * veda_block_sparse_bwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference.
+ *
+ * Same arguments and results as veda_block_sparse_bwd minus workspace /
+ * workspace_bytes: the per-row statistics go to a 64 MiB device array of the
+ * library instead (one per device, held until the process ends), so
+ * n_heads * n_q_tiles * 2048 bytes must not exceed 64 MiB (32,768
+ * (head, query tile) pairs; BASELINE C2 at 48 heads needs 28,416); larger
+ * calls return VEDA_EINVAL before any launch. The entry point allocates
+ * nothing. The stream must belong to the current device; the first call on
+ * a device looks the array up (hipGetSymbolAddress). Calls that overlap on
+ * one device (different streams, or threads without ordering) share the
+ * array and race: order them on one stream.
+ */
+int veda_block_sparse_bwd_noalloc(
+    const void* q, int64_t q_stride_s, int64_t q_stride_h, const void* k, int64_t k_stride_s,
+    int64_t k_stride_h, const void* v, int64_t v_stride_s, int64_t v_stride_h, const void* out,
+    int64_t o_stride_s, int64_t o_stride_h, const void* dout, int64_t do_stride_s,
+    int64_t do_stride_h, const float* lse, int64_t lse_stride_h, int64_t lse_stride_s,
+    const float* dlse, int64_t dlse_stride_h, int64_t dlse_stride_s, int64_t n_heads,
+    int64_t head_dim, int64_t n_q_tiles, int64_t n_k_tiles, const int32_t* full_cnt,
+    const int32_t* full_idx, const int32_t* part_cnt, const int32_t* part_idx, int64_t list_ld,
+    const int32_t* full_cnt_t, const int32_t* full_idx_t, const int32_t* part_cnt_t,
+    const int32_t* part_idx_t, int64_t list_ld_t, const int32_t* valid_count, float scale,
+    void* dq, int64_t dq_stride_s, int64_t dq_stride_h, void* dk, int64_t dk_stride_s,
+    int64_t dk_stride_h, void* dv, int64_t dv_stride_s, int64_t dv_stride_h,
+    int64_t front_tiles, void* stream);
+
+/*
  * Predictor tile embedding, miowtion/veda/predictor.py:251-255:
  *   out[h', t, :] = feats[h', t, :] @ W[heads[h']] (+ feats[h', t, :n_out]
  *   when residual), fp32 accumulation.

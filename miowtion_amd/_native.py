@@ -48,6 +48,10 @@ SIGNATURES: dict[str, list] = {
                               _P, _I, _I, _P, _I, _I, _I, _I, _I, _I,
                               _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _F,
                               _P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _I, _P],
+    'veda_block_sparse_bwd_noalloc': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I,
+                                      _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I,
+                                      _P, _P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _F,
+                                      _P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _P],
     'veda_compensated_attention': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I,
                                    _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P, _F,
                                    _P, _I, _I, _I, _P],

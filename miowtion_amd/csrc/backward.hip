@@ -35,6 +35,8 @@
 // global_load_lds_dwordx4 (the swizzle is applied by the choice of source
 // address), double-buffered: step u + 1 loads while step u computes.
 
+#include <mutex>
+
 #include "veda_common.h"
 #include "veda_pipeline.h"
 
@@ -652,4 +654,104 @@ extern "C" int veda_block_sparse_bwd(
     return check_launch("veda_block_sparse_bwd (dk, dv)");
   }
   return VEDA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The backward without allocation: the per-row statistics go to a
+// file-scope device array instead of a caller workspace, for callers that
+// cannot allocate device memory (code under HIP graph capture, serving loops,
+// harnesses that forbid hipMalloc).
+//
+// In host code `scratch` names a host-side stand-in, not a device address:
+// every use goes through the address hipGetSymbolAddress returns for the
+// device, looked up once per device (on the first call with that device
+// current) and kept in g_scratch_addr. Each device holds its own copy of the
+// array for the life of the process. Nothing in it must start at zero: the
+// statistics kernel writes every record the gradient kernels read.
+
+namespace veda {
+namespace {
+
+constexpr int64_t kScratchBytes = int64_t(64) << 20;  // 64 MiB
+constexpr int kScratchDevices = 64;
+
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kScratchDevices] = {};
+
+// The device address of `scratch` on the current device, which must be the
+// device of `stream`.
+int scratch_address(void* stream, void** addr) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    set_error("block_sparse_bwd_noalloc: hipGetDevice failed: %s", hipGetErrorString(err));
+    return VEDA_ELAUNCH;
+  }
+  if (stream != nullptr) {
+    int sdev = -1;
+    err = hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &sdev);
+    if (err != hipSuccess) {
+      set_error("block_sparse_bwd_noalloc: hipStreamGetDevice failed: %s",
+                hipGetErrorString(err));
+      return VEDA_ELAUNCH;
+    }
+    VEDA_REQUIRE(sdev == dev,
+                 "block_sparse_bwd_noalloc: the stream belongs to device %d, but device %d is "
+                 "current",
+                 sdev, dev);
+  }
+  VEDA_REQUIRE(dev >= 0 && dev < kScratchDevices,
+               "block_sparse_bwd_noalloc: device %d outside [0, %d)", dev, kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr) {
+      set_error("block_sparse_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                dev, hipGetErrorString(err));
+      return VEDA_ELAUNCH;
+    }
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return VEDA_OK;
+}
+
+}  // namespace
+}  // namespace veda
+
+extern "C" int veda_block_sparse_bwd_noalloc(
+    const void* q, int64_t q_stride_s, int64_t q_stride_h, const void* k, int64_t k_stride_s,
+    int64_t k_stride_h, const void* v, int64_t v_stride_s, int64_t v_stride_h, const void* out,
+    int64_t o_stride_s, int64_t o_stride_h, const void* dout, int64_t do_stride_s,
+    int64_t do_stride_h, const float* lse, int64_t lse_stride_h, int64_t lse_stride_s,
+    const float* dlse, int64_t dlse_stride_h, int64_t dlse_stride_s, int64_t n_heads,
+    int64_t head_dim, int64_t n_q_tiles, int64_t n_k_tiles,
+    const int32_t* full_cnt, const int32_t* full_idx, const int32_t* part_cnt,
+    const int32_t* part_idx, int64_t list_ld, const int32_t* full_cnt_t,
+    const int32_t* full_idx_t, const int32_t* part_cnt_t, const int32_t* part_idx_t,
+    int64_t list_ld_t, const int32_t* valid_count, float scale, void* dq, int64_t dq_stride_s,
+    int64_t dq_stride_h, void* dk, int64_t dk_stride_s, int64_t dk_stride_h, void* dv,
+    int64_t dv_stride_s, int64_t dv_stride_h, int64_t front_tiles, void* stream) {
+  VEDA_REQUIRE(n_heads >= 0 && n_q_tiles >= 0 && n_q_tiles <= kMaxTiles,
+               "block_sparse_bwd_noalloc: bad sizes (%lld heads, %lld query tiles)",
+               (long long)n_heads, (long long)n_q_tiles);
+  const int64_t need = n_heads * 2 * n_q_tiles * kRecBytes;
+  VEDA_REQUIRE(need <= kScratchBytes,
+               "block_sparse_bwd_noalloc: %lld heads x %lld query tiles need %lld bytes of "
+               "statistics, more than its %lld-byte scratch; split the heads or call "
+               "veda_block_sparse_bwd with a workspace",
+               (long long)n_heads, (long long)n_q_tiles, (long long)need,
+               (long long)kScratchBytes);
+  void* work = nullptr;
+  if (int rc = scratch_address(stream, &work)) return rc;
+  return veda_block_sparse_bwd(
+      q, q_stride_s, q_stride_h, k, k_stride_s, k_stride_h, v, v_stride_s, v_stride_h, out,
+      o_stride_s, o_stride_h, dout, do_stride_s, do_stride_h, lse, lse_stride_h, lse_stride_s,
+      dlse, dlse_stride_h, dlse_stride_s, n_heads, head_dim, n_q_tiles, n_k_tiles, full_cnt,
+      full_idx, part_cnt, part_idx, list_ld, full_cnt_t, full_idx_t, part_cnt_t, part_idx_t,
+      list_ld_t, valid_count, scale, dq, dq_stride_s, dq_stride_h, dk, dk_stride_s, dk_stride_h,
+      dv, dv_stride_s, dv_stride_h, work, kScratchBytes, front_tiles, stream);
 }

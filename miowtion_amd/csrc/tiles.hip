@@ -328,7 +328,7 @@ using namespace veda;
 
 extern "C" const char* veda_last_error(void) { return g_error.c_str(); }
 
-extern "C" int veda_abi_version(void) { return 4; }
+extern "C" int veda_abi_version(void) { return 5; }
 
 extern "C" int veda_gather_tiles(const void* x, int64_t x_rows, int64_t x_heads,
                                  int64_t x_stride_s, int64_t x_stride_h,
