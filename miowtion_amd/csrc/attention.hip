@@ -1014,6 +1014,91 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       sstep_virtual(cur, fa, fb, c, vwt, key0, hi, w);
     }
   };
+  if constexpr (MODE == kSparse) {
+    // Step records in registers: lane i of win_a / win_b holds sub-block a /
+    // b of step 64 m + i of the current window m, as (first key row << 6 |
+    // valid keys of the sub-block, clamped to 0 .. 32), decoded from the LDS
+    // step list by all lanes at once, once per 64 steps. A step's record is
+    // read into scalar registers (v_readlane) when its loads are issued, one
+    // step ahead, and carried to its compute, so the loop itself reads no
+    // step list and waits on no LDS read for it.
+    uint32_t win_a = 0, win_b = 0;
+    auto lane_half = [&](int e, int64_t& r0, int& vch) {
+      if (e == kVoidStep) {
+        r0 = 0;
+        vch = 0;
+        return;
+      }
+      const int j = e >> 2, half = (e >> 1) & 1, full = e & 1;
+      const int vc = full ? kTile : (int)tvc[j];
+      r0 = (int64_t)j * kTile + half * kHalf;
+      vch = half ? vc - kHalf : min(vc, kHalf);
+    };
+    auto refill = [&](int base) {
+      const int u = base + lane;
+      int64_t row0 = 0, rowb = 0;
+      int la = 0, lb = 0;
+      if (u < n_big) {
+        lane_half(steps[u], row0, la);
+        rowb = row0 + 32;
+        lb = la - 32;
+      } else if (u < n_lsteps) {
+        const int k = 2 * (u - n_big);
+        lane_half(steps[2 * kMaxBlocks - 1 - k], row0, la);
+        if (k + 1 < n_small) lane_half(steps[2 * kMaxBlocks - 2 - k], rowb, lb);
+      }
+      win_a = ((uint32_t)row0 << 6) | (uint32_t)min(max(la, 0), 32);
+      win_b = ((uint32_t)rowb << 6) | (uint32_t)min(max(lb, 0), 32);
+    };
+    auto fetch = [&](int u, uint32_t& ra, uint32_t& rb) {
+      if ((u & 63) == 0) refill(u);
+      ra = (uint32_t)__builtin_amdgcn_readlane((int)win_a, u & 63);
+      rb = (uint32_t)__builtin_amdgcn_readlane((int)win_b, u & 63);
+    };
+    // waves 0, 1 load sub-block a, waves 2, 3 sub-block b (rows
+    // 16 (wave & 1) .. + 15 of it); a segment past the sub-block's valid
+    // keys reloads its first rows (not read: masked)
+    auto load_rec = [&](uint32_t ra, uint32_t rb, lds_u8* slot) {
+      const uint32_t rec = wave < 2 ? ra : rb;
+      const int64_t base = (int64_t)(rec >> 6);
+      const int lim = (int)(rec & 63u);
+      const char* kb = reinterpret_cast<const char*>(kbase + base * p.ks);
+      const char* vb = reinterpret_cast<const char*>(vbase + base * p.vs);
+#pragma unroll
+      for (int u4 = 0; u4 < 4; ++u4) {
+        const int seg = 4 * wave + u4;
+        const bool live = 4 * (4 * (wave & 1) + u4) < lim;
+        dma16(kb, live ? dma.k[u4] : dma.k_skip[u4], slot + seg * 1024);
+        dma16(vb, live ? dma.v[u4] : dma.v_skip[u4], slot + kHalfBytes + seg * 1024);
+      }
+    };
+    auto compute = [&](uint32_t ra, uint32_t rb, const lds_u8* cur) {
+      sstep(cur, fa, fb, c, (int)(ra & 63u), (int)(rb & 63u), hi, w);
+    };
+    uint32_t ca = 0, cb = 0;
+    if (n_steps > 0) {
+      fetch(0, ca, cb);
+      load_rec(ca, cb, s0);
+    }
+    for (int u = 0; u < n_steps; u += 2) {
+      uint32_t na = 0, nb = 0;
+      VEDA_WAIT_VM(0);
+      __builtin_amdgcn_s_barrier();
+      if (u + 1 < n_steps) {
+        fetch(u + 1, na, nb);
+        load_rec(na, nb, s1);
+      }
+      compute(ca, cb, s0);
+      if (u + 1 >= n_steps) break;
+      VEDA_WAIT_VM(0);
+      __builtin_amdgcn_s_barrier();
+      if (u + 2 < n_steps) {
+        fetch(u + 2, ca, cb);
+        load_rec(ca, cb, s0);
+      }
+      compute(na, nb, s1);
+    }
+  } else {
   if (n_steps > 0) load_step(0, s0);
   if (!VKEYS) {
     for (int u = 0; u < n_steps; u += 2) {
@@ -1064,6 +1149,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       virtual_step(u, s0);
     }
   }
+  }  // MODE != kSparse
 
   const float l = half_swap_sum(w.l_run);
   // compensation: the kept output is num / den over the kept keys with
