@@ -1,14 +1,23 @@
-"""Request geometry: canvas, frame count and the latent token grid.
+"""Request geometry: from (aspect ratio, duration) to the latent token grid.
 
-Host mirror of `miowtion/h3/geometry.py:1-170`. Tile plans and predictor
-bundles are keyed by the geometry name ('16x9_t37') and only valid for the
-exact token grid a request produces, so the rounding rules are kept as the
-reference states them (they are part of the plan format):
-  - canvas: short edge 768 px, the long edge from the aspect ratio, scaled
-    down to at most 768 * 1344 px, each side to the nearest multiple of 32
-    (geometry.py:31-57);
-  - frames: snapped up to 17 n + 5; latent_t = 5 n + 2 (geometry.py:60-77);
-  - tokens: VAE stride 16, then 1x2x2 patches (geometry.py:112-116).
+Tile plans and predictor bundles are keyed by a geometry name such as
+'16x9_t37' and are valid only for the exact token grid that request
+produces (the reference's rules are `miowtion/h3/geometry.py:12-169`). This
+module states those rules as data:
+
+  CanvasRule   the pixel canvas of an aspect ratio: the short edge at 768,
+               the long edge from the ratio, the area capped at 768 x 1344
+               (both edges shrunk by the same factor), each edge rounded to
+               the nearest multiple of 32; ratios outside [1:4, 4:1] refused;
+  FrameLadder  the frame counts the video VAE accepts, 17 n + 5, and their
+               latent frame counts 5 n + 2 (rung n of the ladder);
+  RequestRules the two plus the frame rate (24) and the token edge in pixels
+               (32: VAE stride 16 times the 1x2x2 patch),
+
+and `H3` is the rule set of the H3 model. The functions below keep the
+reference's names so that callers and plan files read the same; only the
+video side exists here (the audio latents play no part in the attention
+path).
 """
 
 from __future__ import annotations
@@ -16,88 +25,96 @@ from __future__ import annotations
 import dataclasses
 import math
 
-FPS = 24
-BASE_SHORT_EDGE = 768
-MAX_PIXELS = BASE_SHORT_EDGE * 1344
-CANVAS_MULTIPLE = 32
-MIN_ASPECT_RATIO = 1.0 / 4.0
-MAX_ASPECT_RATIO = 4.0
-VAE_SPATIAL_STRIDE = 16
-PATCH_HW = 2
-AUDIO_LATENT_HZ = 40.0
-AUDIO_CHANNELS = 2
-MAX_DURATION_SECONDS = 15.0
+
+@dataclasses.dataclass(frozen=True)
+class CanvasRule:
+    """The pixel canvas of an aspect ratio."""
+
+    short_edge: int = 768
+    pixel_budget: int = 768 * 1344   # fixed, whatever short edge is asked for
+    multiple: int = 32
+    widest: float = 4.0              # ratios in [1 / widest, widest]
+
+    def snap(self, pixels: float) -> int:
+        """Nearest multiple (Python rounding, at least one multiple)."""
+        return max(self.multiple, self.multiple * int(round(float(pixels) / self.multiple)))
+
+    def size(self, aspect_w: int, aspect_h: int, short_edge: int | None = None) -> tuple[int, int]:
+        """(width, height) in pixels.
+
+        Raises:
+            ValueError: If the ratio is outside [1 / widest, widest].
+        """
+        edge = float(self.short_edge if short_edge is None else short_edge)
+        ratio = float(aspect_w) / float(aspect_h)
+        if ratio < 1.0 / self.widest or ratio > self.widest:
+            raise ValueError(f'aspect {aspect_w}:{aspect_h} is outside 1:{self.widest:g} .. '
+                             f'{self.widest:g}:1')
+        dims = [edge * ratio, edge] if ratio >= 1.0 else [edge, edge / ratio]
+        area = dims[0] * dims[1]
+        if area > self.pixel_budget:
+            shrink = math.sqrt(float(self.pixel_budget) / area)
+            dims = [d * shrink for d in dims]
+        return self.snap(dims[0]), self.snap(dims[1])
 
 
-def _nearest_multiple(value: float, multiple: int) -> int:
-    return max(multiple, int(round(float(value) / multiple)) * multiple)
+@dataclasses.dataclass(frozen=True)
+class FrameLadder:
+    """Rung n holds period * n + first frames and latent_step * n +
+    latent_first latent frames."""
 
+    period: int = 17
+    first: int = 5
+    latent_step: int = 5
+    latent_first: int = 2
 
-def resolve_canvas(aspect_w: int, aspect_h: int,
-                   short_edge: int = BASE_SHORT_EDGE) -> tuple[int, int]:
-    """(width, height) in pixels, both multiples of 32 (geometry.py:31-57).
+    def frames(self, rung: int) -> int:
+        return self.period * rung + self.first
 
-    Raises:
-        ValueError: If the ratio is outside [1:4, 4:1].
-    """
-    ratio = float(aspect_w) / float(aspect_h)
-    if not MIN_ASPECT_RATIO <= ratio <= MAX_ASPECT_RATIO:
-        raise ValueError(f'aspect ratio {aspect_w}:{aspect_h} out of range')
-    if ratio >= 1.0:
-        width, height = float(short_edge) * ratio, float(short_edge)
-    else:
-        width, height = float(short_edge), float(short_edge) / ratio
-    area = width * height
-    if area > MAX_PIXELS:
-        shrink = math.sqrt(float(MAX_PIXELS) / area)
-        width, height = width * shrink, height * shrink
-    return _nearest_multiple(width, CANVAS_MULTIPLE), _nearest_multiple(height, CANVAS_MULTIPLE)
+    def latent(self, rung: int) -> int:
+        return self.latent_step * rung + self.latent_first
 
+    def rung_up(self, frames: int) -> int:
+        """The lowest rung with at least `frames` frames."""
+        return max(0, -(-(int(frames) - self.first) // self.period))
 
-def align_frame_count(frame_count: int) -> int:
-    """Frame count snapped up to 17 n + 5 (1 for non-positive input)."""
-    if frame_count <= 0:
-        return 1
-    return int(frame_count) + (5 - int(frame_count)) % 17
+    def rung_down(self, frames: int) -> int:
+        """The highest rung with at most `frames` frames (rung 0 below it)."""
+        return max(0, (int(frames) - self.first) // self.period)
 
-
-def video_latent_t(frame_count: int) -> int:
-    if frame_count <= 5:
-        return 2
-    return ((int(frame_count) - 5) // 17) * 5 + 2
-
-
-def frame_count_from_latent_t(latent_t: int) -> int:
-    if latent_t < 2 or (latent_t - 2) % 5:
-        raise ValueError(f'latent_t {latent_t} is not of the form 5n+2')
-    return 17 * ((latent_t - 2) // 5) + 5
-
-
-def audio_latent_t(duration_seconds: float) -> int:
-    return int(round(float(duration_seconds) * AUDIO_LATENT_HZ))
+    def rung_of_latent(self, latent_t: int) -> int:
+        """Raises ValueError unless latent_t is latent_step * n + latent_first."""
+        rung, rest = divmod(int(latent_t) - self.latent_first, self.latent_step)
+        if rung < 0 or rest:
+            raise ValueError(f'latent_t {latent_t} is not {self.latent_step} n + '
+                             f'{self.latent_first}')
+        return rung
 
 
 @dataclasses.dataclass(frozen=True)
 class Geometry:
-    """A resolved target geometry (geometry.py:85-131)."""
+    """A resolved request: canvas, frame count and the latent token grid."""
 
     aspect: str
     width: int
     height: int
     frame_count: int
     latent_t: int
-    latent_h: int
-    latent_w: int
-    audio_t: int
+    token_px: int = 32
+    fps: int = 24
 
     @property
-    def duration_seconds(self) -> float:
-        return self.frame_count / FPS
+    def latent_h(self) -> int:
+        return self.height // (self.token_px // 2)
+
+    @property
+    def latent_w(self) -> int:
+        return self.width // (self.token_px // 2)
 
     @property
     def video_grid(self) -> tuple[int, int, int]:
-        """Token grid (T, H, W) of the target video after 1x2x2 patching."""
-        return self.latent_t, self.latent_h // PATCH_HW, self.latent_w // PATCH_HW
+        """Token grid (T, H, W) of the target video."""
+        return self.latent_t, self.height // self.token_px, self.width // self.token_px
 
     @property
     def num_video_tokens(self) -> int:
@@ -105,43 +122,81 @@ class Geometry:
         return t * h * w
 
     @property
-    def num_audio_rows(self) -> int:
-        return AUDIO_CHANNELS * self.audio_t
+    def duration_seconds(self) -> float:
+        return self.frame_count / self.fps
 
     @property
     def name(self) -> str:
-        """Stable key, e.g. '16x9_t37'."""
-        return f'{self.aspect.replace(":", "x")}_t{self.latent_t}'
+        """The key plans and bundles use, '<w>x<h>_t<latent_t>'."""
+        return '%s_t%d' % (self.aspect.replace(':', 'x'), self.latent_t)
+
+
+@dataclasses.dataclass(frozen=True)
+class RequestRules:
+    fps: int = 24
+    canvas: CanvasRule = CanvasRule()
+    ladder: FrameLadder = FrameLadder()
+    token_px: int = 32
+
+    def snap_frames(self, frames: int) -> int:
+        """Requested frames snapped up onto the ladder (1 if none)."""
+        return 1 if frames <= 0 else self.ladder.frames(self.ladder.rung_up(frames))
+
+    def geometry(self, aspect: str, seconds: float, short_edge: int | None = None) -> Geometry:
+        aw, ah = (int(x) for x in aspect.split(':'))
+        width, height = self.canvas.size(aw, ah, short_edge)
+        frames = self.snap_frames(int(round(float(seconds) * self.fps)))
+        return Geometry(aspect, width, height, frames,
+                        self.ladder.latent(self.ladder.rung_down(frames)), self.token_px, self.fps)
+
+    def at_latent(self, aspect: str, latent_t: int, short_edge: int | None = None) -> Geometry:
+        """The geometry of a request exactly as long as latent_t's rung."""
+        frames = self.ladder.frames(self.ladder.rung_of_latent(latent_t))
+        return self.geometry(aspect, frames / self.fps, short_edge)
+
+    def reachable(self, min_seconds: float, max_seconds: float) -> list[int]:
+        """latent_t of every rung whose duration lies in [min, max] seconds."""
+        out, rung = [], 0
+        while self.ladder.frames(rung) / self.fps <= max_seconds:
+            if self.ladder.frames(rung) / self.fps >= min_seconds:
+                out.append(self.ladder.latent(rung))
+            rung += 1
+        return out
+
+
+H3 = RequestRules()
+FPS = H3.fps
+BASE_SHORT_EDGE = H3.canvas.short_edge
+MAX_DURATION_SECONDS = 15.0
+
+
+def resolve_canvas(aspect_w: int, aspect_h: int,
+                   short_edge: int = BASE_SHORT_EDGE) -> tuple[int, int]:
+    return H3.canvas.size(aspect_w, aspect_h, short_edge)
+
+
+def align_frame_count(frame_count: int) -> int:
+    return H3.snap_frames(frame_count)
+
+
+def video_latent_t(frame_count: int) -> int:
+    return H3.ladder.latent(H3.ladder.rung_down(frame_count))
+
+
+def frame_count_from_latent_t(latent_t: int) -> int:
+    return H3.ladder.frames(H3.ladder.rung_of_latent(latent_t))
 
 
 def resolve_geometry(aspect: str, duration_seconds: float,
                      short_edge: int = BASE_SHORT_EDGE) -> Geometry:
-    """(aspect, requested duration) -> geometry (geometry.py:134-148)."""
-    aspect_w, aspect_h = (int(v) for v in aspect.split(':'))
-    width, height = resolve_canvas(aspect_w, aspect_h, short_edge)
-    frame_count = align_frame_count(int(round(float(duration_seconds) * FPS)))
-    return Geometry(aspect=aspect, width=width, height=height, frame_count=frame_count,
-                    latent_t=video_latent_t(frame_count),
-                    latent_h=height // VAE_SPATIAL_STRIDE,
-                    latent_w=width // VAE_SPATIAL_STRIDE,
-                    audio_t=audio_latent_t(frame_count / FPS))
+    return H3.geometry(aspect, duration_seconds, short_edge)
 
 
 def geometry_from_latent_t(aspect: str, latent_t: int,
                            short_edge: int = BASE_SHORT_EDGE) -> Geometry:
-    """The geometry whose duration is exactly frame_count / FPS."""
-    return resolve_geometry(aspect, frame_count_from_latent_t(latent_t) / FPS, short_edge)
+    return H3.at_latent(aspect, latent_t, short_edge)
 
 
 def latent_t_ladder(min_seconds: float = 5.0,
                     max_seconds: float = MAX_DURATION_SECONDS) -> list[int]:
-    """Every reachable latent_t whose duration lies in [min, max] seconds."""
-    ladder = []
-    latent_t = 2
-    while True:
-        seconds = frame_count_from_latent_t(latent_t) / FPS
-        if seconds > max_seconds:
-            return ladder
-        if seconds >= min_seconds:
-            ladder.append(latent_t)
-        latent_t += 5
+    return H3.reachable(min_seconds, max_seconds)

@@ -216,3 +216,42 @@ def test_random_bundle_uses_least_padding_uniform_plans():
         assert plan.geometry == g.name and plan.shapes == [pt.least_padding_shape(g.video_grid)]
         assert plan.head_shape == [[0] * 4, [0] * 4]
     assert isinstance(b.predictor, pp.TileScorePredictor) and b.keep_ratio == 0.1
+
+
+def test_bundle_metadata_is_the_reference_format(tmp_path):
+    """Every metadata key and value a 'miowtion-veda-predictor-v1' writer
+    puts in the file (the format of miowtion/veda/bundle.py:215-235): the
+    strings, the sorted plans JSON and the legacy keep_ratio."""
+    w = _weights(layers=1)
+    path = str(tmp_path / 'b.safetensors')
+    table = _table()
+    bundle.save(path, w, table, num_layers=1, num_heads=4, head_dim=128, keep_ratio=0.25,
+                ref_keep_tiles=7.0, tile_conditions=True, source='ckpt/run', source_weights='live',
+                step=12, dtype=torch.bfloat16, second_order_rank=0, count_term=False)
+    meta = bundle.read_metadata(path)
+    want_plans = json.dumps({name: p.to_json() for name, p in sorted(table.plans.items())})
+    assert meta == {
+        'format': 'miowtion-veda-predictor-v1', 'num_layers': '1', 'num_heads': '4',
+        'head_dim': '128', 'dtype': 'bfloat16', 'tile_conditions': 'true', 'source': 'ckpt/run',
+        'source_weights': 'live', 'step': '12', 'second_order_rank': '0', 'count_term': '0',
+        'plans': want_plans, 'target_budget_kind': 'ratio', 'target_budget_value': '0.25',
+        'ref_budget_kind': 'tiles', 'ref_budget_value': '7.0', 'keep_ratio': '0.25'}
+    # the tensors: bare state-dict names, stored in the requested dtype
+    from safetensors import safe_open
+    with safe_open(path, framework='pt', device='cpu') as f:
+        assert sorted(f.keys()) == ['layers.0.proj_k', 'layers.0.proj_q']
+        assert f.get_tensor('layers.0.proj_q').dtype == torch.bfloat16
+
+
+def test_plan_json_round_trips_the_released_file_unchanged(tmp_path):
+    raw = json.loads((GOLDEN / 'plan_16x9_t37.json').read_text())
+    plan = pplan.TilePlan.from_json(raw)
+    assert plan.to_json() == raw
+    out = tmp_path / 'p.json'
+    plan.save(str(out))
+    assert json.loads(out.read_text()) == raw
+    assert [p.name for p in tmp_path.iterdir()] == ['p.json']   # no temporary left behind
+    with pytest.raises(ValueError, match='at most 2'):
+        pplan.TilePlan('g', (1, 8, 16), [pt.TileShape.parse(s) for s in ('1x8x16', '2x8x8',
+                                                                             '4x4x8')],
+                       [[0, 1, 2]])
