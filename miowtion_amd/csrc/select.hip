@@ -15,6 +15,8 @@
 // Lists: one wave per (head, row), 64 columns per step, positions from a
 // ballot + popcount prefix (no sort, no atomics).
 
+#include <type_traits>
+
 #include "veda_common.h"
 
 namespace veda {
@@ -147,19 +149,91 @@ __global__ void __launch_bounds__(256) dense_mask_kernel(
   for (int c = threadIdx.x; c < n_tiles; c += blockDim.x) out[c] = row[c];
 }
 
-__global__ void __launch_bounds__(256) index_lists_kernel(
-    const uint8_t* __restrict__ mask, int64_t n_items, int n_tiles,
+// Index lists: one wave per (head, row). The row's classes (0 outside the
+// row's members, 1 full member, 2 partial member) are first staged in LDS
+// with wide independent loads; the lists are then written 64 columns at a
+// time, each lane storing its column once per list (members at their rank,
+// non-members after all members), so every store instruction is whole.
+// Rows longer than kListCols take the two-pass form from global memory.
+constexpr int kListWaves = 4;
+constexpr int kListCols = 4096;
+
+template <int VEC>
+__device__ __forceinline__ void stage_classes(const uint8_t* __restrict__ m,
+                                              const uint8_t* __restrict__ kv_ok,
+                                              const uint8_t* __restrict__ full_tile, int n_tiles,
+                                              int lane, uint8_t* cls, int& counts) {
+  using Vec = typename std::conditional<VEC == 16, uint4,
+              typename std::conditional<VEC == 4, uint32_t, uint8_t>::type>::type;
+  int nf = 0, np = 0;
+#pragma unroll 4
+  for (int c = lane * VEC; c < n_tiles; c += 64 * VEC) {
+    union { Vec v; uint8_t b[VEC]; } mm, kk, ff, out;
+    mm.v = *reinterpret_cast<const Vec*>(m + c);
+    kk.v = *reinterpret_cast<const Vec*>(kv_ok + c);
+    ff.v = *reinterpret_cast<const Vec*>(full_tile + c);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const bool member = mm.b[j] && kk.b[j];
+      const bool full = ff.b[j] != 0;
+      out.b[j] = member ? (full ? 1 : 2) : 0;
+      nf += member && full;
+      np += member && !full;
+    }
+    *reinterpret_cast<Vec*>(cls + c) = out.v;
+  }
+  counts = nf | (np << 16);  // both at most 4096
+}
+
+__global__ void __launch_bounds__(64 * kListWaves) index_lists_kernel(
+    const uint8_t* __restrict__ mask, int64_t n_items, int n_tiles, int vec,
     const uint8_t* __restrict__ kv_ok, const uint8_t* __restrict__ full_tile,
     int32_t* __restrict__ part_cnt, int32_t* __restrict__ part_idx,
     int32_t* __restrict__ full_cnt, int32_t* __restrict__ full_idx) {
+  __shared__ __align__(16) uint8_t cls_lds[kListWaves][kListCols];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
-  if (item >= n_items) return;
+  const int64_t item = (int64_t)blockIdx.x * kListWaves + wave;
+  if (item >= n_items) return;  // each wave uses only its own LDS row
   const uint8_t* m = mask + item * n_tiles;
   int32_t* fi = full_idx + item * n_tiles;
   int32_t* pi = part_idx + item * n_tiles;
   const uint64_t below = (1ull << lane) - 1ull;
+  if (n_tiles <= kListCols) {
+    uint8_t* cls = cls_lds[wave];
+    int counts;
+    if (vec == 16)
+      stage_classes<16>(m, kv_ok, full_tile, n_tiles, lane, cls, counts);
+    else if (vec == 4)
+      stage_classes<4>(m, kv_ok, full_tile, n_tiles, lane, cls, counts);
+    else
+      stage_classes<1>(m, kv_ok, full_tile, n_tiles, lane, cls, counts);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) counts += __shfl_xor(counts, off);
+    const int NF = counts & 0xffff, NP = counts >> 16;
+    // the lanes' LDS stores are seen by the other lanes of this wave
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int nf = 0, np = 0;  // members before the chunk
+    for (int c0 = 0; c0 < n_tiles; c0 += 64) {
+      const int c = c0 + lane;
+      const int k = c < n_tiles ? cls[c] : 0;
+      const uint64_t bf = __ballot(k == 1), bp = __ballot(k == 2);
+      const int rf = __popcll(bf & below), rp = __popcll(bp & below);
+      if (c < n_tiles) {
+        fi[k == 1 ? nf + rf : NF + (c0 - nf) + (lane - rf)] = c;
+        pi[k == 2 ? np + rp : NP + (c0 - np) + (lane - rp)] = c;
+      }
+      nf += __popcll(bf);
+      np += __popcll(bp);
+    }
+    if (lane == 0) {
+      full_cnt[item] = NF;
+      part_cnt[item] = NP;
+    }
+    return;
+  }
   int nf = 0, np = 0;
   for (int c0 = 0; c0 < n_tiles; c0 += 64) {
     const int c = c0 + lane;
@@ -250,7 +324,15 @@ extern "C" int veda_index_lists(const uint8_t* block_mask, int64_t n_heads, int6
   const int64_t items = n_heads * n_rows;
   if (items == 0) return VEDA_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  index_lists_kernel<<<(unsigned)((items + 3) / 4), 256, 0, s>>>(
-      block_mask, items, (int)n_tiles, kv_ok, full_tile, part_cnt, part_idx, full_cnt, full_idx);
+  // widest load every row start and both column tables allow
+  auto aligned = [&](int64_t a) {
+    return n_tiles % a == 0 && reinterpret_cast<uintptr_t>(block_mask) % a == 0 &&
+           reinterpret_cast<uintptr_t>(kv_ok) % a == 0 &&
+           reinterpret_cast<uintptr_t>(full_tile) % a == 0;
+  };
+  const int vec = aligned(16) ? 16 : aligned(4) ? 4 : 1;
+  index_lists_kernel<<<(unsigned)((items + kListWaves - 1) / kListWaves), 64 * kListWaves, 0,
+                       s>>>(block_mask, items, (int)n_tiles, vec, kv_ok, full_tile, part_cnt,
+                            part_idx, full_cnt, full_idx);
   return check_launch("veda_index_lists");
 }

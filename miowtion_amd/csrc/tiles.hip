@@ -47,6 +47,8 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kSlotsPerWave = kTile / kWaves;  // 32
+constexpr int kCopyWaves = 16;                 // waves of the plain gather and the scatter
+constexpr int kPoolWaves = 4;                  // waves of the pooled gather (8 measured slower)
 
 struct Row8 {
   uint32_t w[4];  // 8 bf16 values
@@ -62,13 +64,31 @@ __device__ __forceinline__ void store_row8(uint16_t* p, const Row8& r) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
 
+
+// Streaming forms for rows touched once: the non-temporal hint keeps the
+// copy streams from displacing other lines in the caches.
+__device__ __forceinline__ Row8 load_row8_nt(const uint16_t* p) {
+  u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return Row8{{v[0], v[1], v[2], v[3]}};
+}
+
+__device__ __forceinline__ void store_row8_nt(uint16_t* p, const Row8& r) {
+  u32x4 v = {r.w[0], r.w[1], r.w[2], r.w[3]};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
 __device__ __forceinline__ float elem(const Row8& r, int e) {
   uint32_t w = r.w[e >> 1];
   return bf16_to_f32((e & 1) ? (w >> 16) : (w & 0xffffu));
 }
 
-template <int D, bool POOL, bool SECOND>
-__global__ void __launch_bounds__(256) gather_kernel(
+// Gather. Workgroup = (tile, group of heads) with WAVES waves, each on
+// 128 / WAVES consecutive slots; lane = (head, 16-byte chunk). More waves
+// per tile put more rows in flight per workgroup: the plain copy runs with
+// kCopyWaves, the pooling with kPoolWaves (its per-wave partials go through
+// LDS, [stat][wave][lane][8]), the variance pass with kWaves.
+template <int D, bool POOL, bool SECOND, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) gather_kernel(
     const uint16_t* __restrict__ x, int64_t x_rows, int64_t x_heads,
     int64_t xs, int64_t xh, const int64_t* __restrict__ gather_index,
     const int32_t* __restrict__ slot_valid,
@@ -89,7 +109,9 @@ __global__ void __launch_bounds__(256) gather_kernel(
   const bool head_ok = hp < n_heads;
   const int64_t head = head_ok ? heads[hp] : 0;
   const bool src_head_ok = head_ok && head >= 0 && head < x_heads;
-  const int64_t slot0 = (int64_t)tile * kTile + wave * kSlotsPerWave;
+  constexpr int kSlots = kTile / WAVES;  // slots per wave
+  static_assert(!SECOND || WAVES == kWaves, "the variance pass runs on kWaves waves");
+  const int64_t slot0 = (int64_t)tile * kTile + wave * kSlots;
   const int count = POOL ? valid_count[tile] : 0;
 
   float s_sum[8], s_max[8], s_min[8], s_sq[8];
@@ -102,15 +124,17 @@ __global__ void __launch_bounds__(256) gather_kernel(
   }
 
 #pragma unroll 8
-  for (int i = 0; i < kSlotsPerWave; ++i) {
+  for (int i = 0; i < kSlots; ++i) {
     const int64_t slot = slot0 + i;
     const int64_t src = gather_index[slot];
     const bool ok = slot_valid[slot] != 0 && src_head_ok && src >= 0 && src < x_rows;
     Row8 r = {{0u, 0u, 0u, 0u}};
-    if (ok) r = load_row8(x + src * xs + head * xh + chunk * 8);
-    if (head_ok && out != nullptr) store_row8(out + slot * os + hp * oh + chunk * 8, r);
+    // the variance pass re-reads the tile, so it keeps the plain load
+    if (ok) r = SECOND ? load_row8(x + src * xs + head * xh + chunk * 8)
+                       : load_row8_nt(x + src * xs + head * xh + chunk * 8);
+    if (head_ok && out != nullptr) store_row8_nt(out + slot * os + hp * oh + chunk * 8, r);
     if (POOL) {
-      const bool real = (wave * kSlotsPerWave + i) < count;
+      const bool real = (wave * kSlots + i) < count;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float f = elem(r, e);
@@ -127,7 +151,7 @@ __global__ void __launch_bounds__(256) gather_kernel(
 
   // Cross-wave reduction through LDS: [stat][wave][lane][8].
   constexpr int kStats = SECOND ? 4 : 3;
-  __shared__ float red[kStats][kWaves][64][8];
+  __shared__ float red[kStats][WAVES][64][8];
   __shared__ float mean_lds[64][8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -147,7 +171,7 @@ __global__ void __launch_bounds__(256) gather_kernel(
       float a = red[0][0][lane][e], b = red[1][0][lane][e], c = red[2][0][lane][e];
       float d = SECOND ? red[kStats - 1][0][lane][e] : 0.f;
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w) {
+      for (int w = 1; w < WAVES; ++w) {
         a += red[0][w][lane][e];
         b = fmaxf(b, red[1][w][lane][e]);
         c = fminf(c, red[2][w][lane][e]);
@@ -184,9 +208,9 @@ __global__ void __launch_bounds__(256) gather_kernel(
     acc[e] = 0.f;
   }
 #pragma unroll 8
-  for (int i = 0; i < kSlotsPerWave; ++i) {
+  for (int i = 0; i < kSlots; ++i) {
     const int64_t slot = slot0 + i;
-    if (wave * kSlotsPerWave + i >= count) break;
+    if (wave * kSlots + i >= count) break;
     const int64_t src = gather_index[slot];
     const bool ok = slot_valid[slot] != 0 && src_head_ok && src >= 0 && src < x_rows;
     Row8 r = {{0u, 0u, 0u, 0u}};
@@ -206,7 +230,7 @@ __global__ void __launch_bounds__(256) gather_kernel(
     for (int e = 0; e < 8; ++e) {
       float a = red[0][0][lane][e];
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w) a += red[0][w][lane][e];
+      for (int w = 1; w < WAVES; ++w) a += red[0][w][lane][e];
       v[e] = empty ? 0.f : a / denom;
     }
     float* o = var + fbase * D + chunk * 8;
@@ -215,8 +239,8 @@ __global__ void __launch_bounds__(256) gather_kernel(
   }
 }
 
-template <int D>
-__global__ void __launch_bounds__(256) scatter_kernel(
+template <int D, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) scatter_kernel(
     const uint16_t* __restrict__ tiled, int64_t ts, int64_t th,
     const int64_t* __restrict__ scatter_index,
     const int32_t* __restrict__ slot_valid, const int64_t* __restrict__ heads,
@@ -233,14 +257,15 @@ __global__ void __launch_bounds__(256) scatter_kernel(
   if (hp >= n_heads) return;
   const int64_t head = heads[hp];
   if (head < 0 || head >= out_heads) return;
-  const int64_t slot0 = (int64_t)tile * kTile + wave * kSlotsPerWave;
+  constexpr int kSlots = kTile / WAVES;
+  const int64_t slot0 = (int64_t)tile * kTile + wave * kSlots;
 #pragma unroll 8
-  for (int i = 0; i < kSlotsPerWave; ++i) {
+  for (int i = 0; i < kSlots; ++i) {
     const int64_t slot = slot0 + i;
     const int64_t dst = scatter_index[slot];
     if (slot_valid[slot] == 0 || dst < 0 || dst >= out_rows) continue;
-    Row8 r = load_row8(tiled + slot * ts + hp * th + chunk * 8);
-    store_row8(out + dst * os + head * oh + chunk * 8, r);
+    Row8 r = load_row8_nt(tiled + slot * ts + hp * th + chunk * 8);
+    store_row8_nt(out + dst * os + head * oh + chunk * 8, r);
   }
 }
 
@@ -355,19 +380,18 @@ extern "C" int veda_gather_tiles(const void* x, int64_t x_rows, int64_t x_heads,
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   auto xx = static_cast<const uint16_t*>(x);
   auto oo = static_cast<uint16_t*>(out);
-#define VEDA_GATHER(D, P, S2)                                                                  \
-  gather_kernel<D, P, S2><<<grid, 256, 0, s>>>(xx, x_rows, x_heads, x_stride_s, x_stride_h,   \
-                                               gather_index, slot_valid, valid_count, n_tiles, \
-                                               heads, n_heads, oo, out_stride_s, out_stride_h, \
-                                               feats, sq, var)
+#define VEDA_GATHER(D, P, S2, W)                                                              \
+  gather_kernel<D, P, S2, W><<<grid, 64 * W, 0, s>>>(                                          \
+      xx, x_rows, x_heads, x_stride_s, x_stride_h, gather_index, slot_valid, valid_count,      \
+      n_tiles, heads, n_heads, oo, out_stride_s, out_stride_h, feats, sq, var)
   if (head_dim == 128) {
-    if (!feats) VEDA_GATHER(128, false, false);
-    else if (!sq) VEDA_GATHER(128, true, false);
-    else VEDA_GATHER(128, true, true);
+    if (!feats) VEDA_GATHER(128, false, false, kCopyWaves);
+    else if (!sq) VEDA_GATHER(128, true, false, kPoolWaves);
+    else VEDA_GATHER(128, true, true, kWaves);
   } else {
-    if (!feats) VEDA_GATHER(64, false, false);
-    else if (!sq) VEDA_GATHER(64, true, false);
-    else VEDA_GATHER(64, true, true);
+    if (!feats) VEDA_GATHER(64, false, false, kCopyWaves);
+    else if (!sq) VEDA_GATHER(64, true, false, kPoolWaves);
+    else VEDA_GATHER(64, true, true, kWaves);
   }
 #undef VEDA_GATHER
   return check_launch("veda_gather_tiles");
@@ -394,13 +418,13 @@ extern "C" int veda_scatter_tiles(const void* tiled, int64_t tiled_stride_s,
   auto tt = static_cast<const uint16_t*>(tiled);
   auto oo = static_cast<uint16_t*>(out);
   if (head_dim == 128)
-    scatter_kernel<128><<<grid, 256, 0, s>>>(tt, tiled_stride_s, tiled_stride_h, scatter_index,
-                                             slot_valid, heads, n_heads, oo, out_rows, out_heads,
-                                             out_stride_s, out_stride_h);
+    scatter_kernel<128, kCopyWaves><<<grid, 64 * kCopyWaves, 0, s>>>(
+        tt, tiled_stride_s, tiled_stride_h, scatter_index, slot_valid, heads, n_heads, oo,
+        out_rows, out_heads, out_stride_s, out_stride_h);
   else
-    scatter_kernel<64><<<grid, 256, 0, s>>>(tt, tiled_stride_s, tiled_stride_h, scatter_index,
-                                            slot_valid, heads, n_heads, oo, out_rows, out_heads,
-                                            out_stride_s, out_stride_h);
+    scatter_kernel<64, kCopyWaves><<<grid, 64 * kCopyWaves, 0, s>>>(
+        tt, tiled_stride_s, tiled_stride_h, scatter_index, slot_valid, heads, n_heads, oo,
+        out_rows, out_heads, out_stride_s, out_stride_h);
   return check_launch("veda_scatter_tiles");
 }
 

@@ -3,12 +3,14 @@ lists: bit-exact against the oracle (which equals torch.topk on distinct
 scores and follows the stable order on ties)."""
 
 import math
+import types
 
 import pytest
 import torch
 
 from miowtion_amd import kernels
 from miowtion_amd import mask as pm
+from miowtion_amd import ops
 from oracle import mask as om
 from oracle import tiling as ot
 from tests import helpers
@@ -78,6 +80,30 @@ def test_index_lists_bit_exact():
     mask = torch.rand(4, lay.n_tiles, lay.n_tiles, generator=g) < 0.4
     got = kernels.index_lists(mask.cuda(), lay)
     want = om.index_lists(mask, olay)
+    for a, b in zip(got, want):
+        assert a.dtype == b.dtype and torch.equal(a.cpu(), b)
+
+
+@pytest.mark.parametrize('n,offset', [(592, 0), (592, 1), (100, 0), (37, 0), (4096, 0),
+                                      (4097, 0), (4160, 0)])
+def test_index_lists_every_load_width(n, offset):
+    """Random masks and column tables whose row length and alignment select
+    each load width of the list kernel (16-, 4- and 1-byte loads; a column
+    table 1 byte off its allocation), and rows past the LDS-staged length
+    (4096 columns): bit-exact against the oracle, counts included."""
+    g = torch.Generator().manual_seed(n + offset)
+    mask = torch.rand(2, 3, n, generator=g) < 0.3
+    mask[1, 2] = False                      # an empty row
+    mask[0, 1] = True                       # a row of all columns
+    kv_ok = torch.rand(n + offset, generator=g) < 0.9
+    full = torch.rand(n + offset, generator=g) < 0.5
+    kv_ok, full = kv_ok[offset:], full[offset:]
+    kv_gpu = torch.zeros(n + offset, dtype=torch.bool, device='cuda')
+    full_gpu = torch.zeros(n + offset, dtype=torch.bool, device='cuda')
+    kv_gpu[offset:] = kv_ok.cuda()
+    full_gpu[offset:] = full.cuda()
+    got = ops.index_lists(mask.cuda(), kv_gpu[offset:], full_gpu[offset:])
+    want = om.index_lists(mask, types.SimpleNamespace(kv_ok=kv_ok, full_tile=full))
     for a, b in zip(got, want):
         assert a.dtype == b.dtype and torch.equal(a.cpu(), b)
 
