@@ -294,7 +294,7 @@ __global__ void __launch_bounds__(256) heat_combine_kernel(
     int64_t n_items, int64_t n_tiles, float* __restrict__ heat) {
   const int64_t item = blockIdx.x;
   const int64_t h = item / n_items, r = item % n_items;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t qt = q_tiles != nullptr ? q_tiles[r] : r;
   const int vc = (qt >= 0 && qt < n_tiles) ? valid_count[qt] : 0;
   float l2[2];

@@ -73,7 +73,7 @@ __global__ void __launch_bounds__(256) select_topk_kernel(
     int64_t n_extra, int64_t* __restrict__ index, uint8_t* __restrict__ keep, int64_t osh,
     int64_t osr, int64_t col0) {
   extern __shared__ uint64_t keys[];  // [kSelWaves][per_lane * 64]
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int64_t item = (int64_t)blockIdx.x * kSelWaves + wave;
   if (item >= n_heads * n_rows) return;  // whole wave exits together
@@ -191,7 +191,7 @@ __global__ void __launch_bounds__(64 * kListWaves) index_lists_kernel(
     int32_t* __restrict__ part_cnt, int32_t* __restrict__ part_idx,
     int32_t* __restrict__ full_cnt, int32_t* __restrict__ full_idx) {
   __shared__ __align__(16) uint8_t cls_lds[kListWaves][kListCols];
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int64_t item = (int64_t)blockIdx.x * kListWaves + wave;
   if (item >= n_items) return;  // each wave uses only its own LDS row

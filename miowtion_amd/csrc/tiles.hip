@@ -48,7 +48,8 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kSlotsPerWave = kTile / kWaves;  // 32
 constexpr int kCopyWaves = 16;                 // waves of the plain gather and the scatter
-constexpr int kPoolWaves = 4;                  // waves of the pooled gather (8 measured slower)
+constexpr int kPoolUnroll = 4;                 // rows in flight per wave of the pooled gather
+constexpr int kPoolOccupancy = 8;              // its waves per SIMD (caps its registers)
 
 struct Row8 {
   uint32_t w[4];  // 8 bf16 values
@@ -85,8 +86,8 @@ __device__ __forceinline__ float elem(const Row8& r, int e) {
 // Gather. Workgroup = (tile, group of heads) with WAVES waves, each on
 // 128 / WAVES consecutive slots; lane = (head, 16-byte chunk). More waves
 // per tile put more rows in flight per workgroup: the plain copy runs with
-// kCopyWaves, the pooling with kPoolWaves (its per-wave partials go through
-// LDS, [stat][wave][lane][8]), the variance pass with kWaves.
+// kCopyWaves; the variance pass (pooling with second moments, whose per-wave
+// partials go through LDS, [stat][wave][lane][8]) with kWaves.
 template <int D, bool POOL, bool SECOND, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES) gather_kernel(
     const uint16_t* __restrict__ x, int64_t x_rows, int64_t x_heads,
@@ -101,7 +102,7 @@ __global__ void __launch_bounds__(64 * WAVES) gather_kernel(
   const int n_groups = (int)((n_heads + kHeadsPerGroup - 1) / kHeadsPerGroup);
   const int tile = (int)(blockIdx.x / n_groups);
   const int group = (int)(blockIdx.x % n_groups);
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int hl = lane / kChunks;
   const int chunk = lane % kChunks;
@@ -239,6 +240,127 @@ __global__ void __launch_bounds__(64 * WAVES) gather_kernel(
   }
 }
 
+// bf16 pairs as int16 pairs whose signed order is the numeric order (the
+// magnitude bits of negative values flipped; -0 orders below +0): max and
+// min of raw rows in packed integer instructions. The map is an involution.
+using s16x2 = short __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ s16x2 order_key(s16x2 v) {
+  return v ^ ((v >> (short)15) & (short)0x7fff);
+}
+
+__device__ __forceinline__ void pool_keys(const Row8& r, s16x2* k_max, s16x2* k_min) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const s16x2 k = order_key(__builtin_bit_cast(s16x2, r.w[w]));
+    k_max[w] = __builtin_elementwise_max(k_max[w], k);
+    k_min[w] = __builtin_elementwise_min(k_min[w], k);
+  }
+}
+
+// Gather with first-order pooling: one wave per (tile, group of heads),
+// over all 128 slots of the tile, so the pooled statistics stay in the
+// lane's registers (no cross-wave reduction, no barrier); the workgroup's
+// waves take consecutive head groups of one tile (adjacent bytes of each
+// source row).
+template <int D>
+__global__ void __launch_bounds__(64 * kWaves, kPoolOccupancy) pool_gather_kernel(
+    const uint16_t* __restrict__ x, int64_t x_rows, int64_t x_heads,
+    int64_t xs, int64_t xh, const int64_t* __restrict__ gather_index,
+    const int32_t* __restrict__ slot_valid,
+    const int32_t* __restrict__ valid_count, int64_t n_tiles,
+    const int64_t* __restrict__ heads, int64_t n_heads,
+    uint16_t* __restrict__ out, int64_t os, int64_t oh, float* __restrict__ feats) {
+  constexpr int kChunks = D / 8;
+  constexpr int kHeadsPerGroup = 64 / kChunks;
+  const int n_groups = (int)((n_heads + kHeadsPerGroup - 1) / kHeadsPerGroup);
+  const int64_t item =
+      (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (item >= n_tiles * n_groups) return;
+  const int64_t tile = item / n_groups;
+  const int group = (int)(item % n_groups);
+  const int lane = threadIdx.x & 63;
+  const int chunk = lane % kChunks;
+  const int64_t hp = (int64_t)group * kHeadsPerGroup + lane / kChunks;
+  const bool head_ok = hp < n_heads;
+  const int64_t head = head_ok ? heads[hp] : 0;
+  const bool src_head_ok = head_ok && head >= 0 && head < x_heads;
+  // lanes of a missing head read head 0 of the row and keep zeros
+  const int64_t lane_off = (src_head_ok ? head : 0) * xh + chunk * 8;
+  const int count = valid_count[tile];
+  float s_sum[8];
+  s16x2 k_max[4], k_min[4];  // order keys of the bf16 pairs
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_sum[e] = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    k_max[w] = s16x2{-32768, -32768};
+    k_min[w] = s16x2{32767, 32767};
+  }
+  // 8 slots at a time; the slots before `count` are the tile's real rows
+  // (every layout puts them first): max / min over those, the sum over all
+  // (the padding rows are zero).
+#pragma unroll 1
+  for (int i0 = 0; i0 < kTile; i0 += kPoolUnroll) {
+    // wave-uniform slots: the index reads are scalar loads, all issued first
+    int64_t src[kPoolUnroll];
+    bool ok[kPoolUnroll];
+#pragma unroll
+    for (int j = 0; j < kPoolUnroll; ++j) {
+      const int64_t slot = tile * kTile + i0 + j;
+      src[j] = gather_index[slot];
+      ok[j] = slot_valid[slot] != 0;
+    }
+    Row8 r[kPoolUnroll];
+#pragma unroll
+    for (int j = 0; j < kPoolUnroll; ++j) {
+      r[j] = Row8{{0u, 0u, 0u, 0u}};
+      if (ok[j] && src[j] >= 0 && src[j] < x_rows)
+        r[j] = load_row8_nt(x + src[j] * xs + lane_off);
+    }
+    if (!src_head_ok) {
+#pragma unroll
+      for (int j = 0; j < kPoolUnroll; ++j) r[j] = Row8{{0u, 0u, 0u, 0u}};
+    }
+#pragma unroll
+    for (int j = 0; j < kPoolUnroll; ++j)
+      if (head_ok && out != nullptr)
+        store_row8_nt(out + (tile * kTile + i0 + j) * os + hp * oh + chunk * 8, r[j]);
+#pragma unroll
+    for (int j = 0; j < kPoolUnroll; ++j) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_sum[e] += elem(r[j], e);
+      if (i0 + j < count) pool_keys(r[j], k_max, k_min);  // wave-uniform branch
+    }
+  }
+  if (!head_ok) return;
+  const bool empty = count == 0;
+  const float denom = (float)(count > 1 ? count : 1);
+  float* f = feats + (hp * n_tiles + tile) * (3 * D) + chunk * 8;
+  float s_max[8], s_min[8];
+  {
+    Row8 mx, mn;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mx.w[w] = __builtin_bit_cast(uint32_t, order_key(k_max[w]));  // the key map is its own inverse
+      mn.w[w] = __builtin_bit_cast(uint32_t, order_key(k_min[w]));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s_sum[e] = empty ? 0.f : s_sum[e] / denom;
+      s_max[e] = empty ? 0.f : elem(mx, e);
+      s_min[e] = empty ? 0.f : elem(mn, e);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e += 4) {
+    *reinterpret_cast<f32x4*>(f + e) = f32x4{s_sum[e], s_sum[e + 1], s_sum[e + 2], s_sum[e + 3]};
+    *reinterpret_cast<f32x4*>(f + D + e) = f32x4{s_max[e], s_max[e + 1], s_max[e + 2], s_max[e + 3]};
+    *reinterpret_cast<f32x4*>(f + 2 * D + e) =
+        f32x4{s_min[e], s_min[e + 1], s_min[e + 2], s_min[e + 3]};
+  }
+}
+
 template <int D, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES) scatter_kernel(
     const uint16_t* __restrict__ tiled, int64_t ts, int64_t th,
@@ -250,7 +372,7 @@ __global__ void __launch_bounds__(64 * WAVES) scatter_kernel(
   constexpr int kHeadsPerGroup = 64 / kChunks;
   const int n_groups = (int)((n_heads + kHeadsPerGroup - 1) / kHeadsPerGroup);
   const int tile = (int)(blockIdx.x / n_groups);
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int64_t hp = (int64_t)(blockIdx.x % n_groups) * kHeadsPerGroup + lane / kChunks;
   const int chunk = lane % kChunks;
@@ -298,7 +420,7 @@ __global__ void __launch_bounds__(256) summary_kernel(
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t cs, int64_t ch) {
   constexpr int kChunks = 16;  // D = 128
   const int tile = blockIdx.x;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int64_t head = (int64_t)blockIdx.y * 4 + lane / kChunks;
   const int chunk = lane % kChunks;
   const bool head_ok = head < n_heads;
@@ -384,16 +506,21 @@ extern "C" int veda_gather_tiles(const void* x, int64_t x_rows, int64_t x_heads,
   gather_kernel<D, P, S2, W><<<grid, 64 * W, 0, s>>>(                                          \
       xx, x_rows, x_heads, x_stride_s, x_stride_h, gather_index, slot_valid, valid_count,      \
       n_tiles, heads, n_heads, oo, out_stride_s, out_stride_h, feats, sq, var)
+#define VEDA_POOL_GATHER(D)                                                                   \
+  pool_gather_kernel<D><<<(unsigned)((n_wg + kWaves - 1) / kWaves), 64 * kWaves, 0, s>>>(      \
+      xx, x_rows, x_heads, x_stride_s, x_stride_h, gather_index, slot_valid, valid_count,      \
+      n_tiles, heads, n_heads, oo, out_stride_s, out_stride_h, feats)
   if (head_dim == 128) {
     if (!feats) VEDA_GATHER(128, false, false, kCopyWaves);
-    else if (!sq) VEDA_GATHER(128, true, false, kPoolWaves);
+    else if (!sq) VEDA_POOL_GATHER(128);
     else VEDA_GATHER(128, true, true, kWaves);
   } else {
     if (!feats) VEDA_GATHER(64, false, false, kCopyWaves);
-    else if (!sq) VEDA_GATHER(64, true, false, kPoolWaves);
+    else if (!sq) VEDA_POOL_GATHER(64);
     else VEDA_GATHER(64, true, true, kWaves);
   }
 #undef VEDA_GATHER
+#undef VEDA_POOL_GATHER
   return check_launch("veda_gather_tiles");
 }
 
