@@ -37,6 +37,8 @@
 
 #include <mutex>
 
+#include <type_traits>
+
 #include "veda_common.h"
 #include "veda_pipeline.h"
 
@@ -457,8 +459,10 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
   // Phase 1: S and P (P-wave) or dP (dS-wave) of both 32-row halves.
   f32x16 sd[2];
   u32x4 pk[2][2];
-  auto phase1 = [&](const lds_u8* slot) {
-    const lds_u8* a = pwave ? slot : slot + kHalfBytes;  // Q or dO rows
+  auto phase1 = [&](auto role, auto full, const lds_u8* slot) __attribute__((always_inline)) {
+    constexpr bool P = decltype(role)::value;
+    constexpr bool FULL = decltype(full)::value;  // every key of the tile valid
+    const lds_u8* a = P ? slot : slot + kHalfBytes;  // Q or dO rows
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
@@ -468,7 +472,7 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
         sd[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(a + qt * 8192 + f.row[s])),
                                                          bf[s], sd[qt], 0, 0, 0);
     }
-    if (!pwave) return;
+    if constexpr (!P) return;
     const lds_u8* sr = slot + kSlot;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
@@ -480,7 +484,7 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           const float x = __builtin_amdgcn_exp2f(fmaf(sd[qt][4 * g + m], c, -l4[m]));
-          p4[m] = key_ok ? x : 0.f;
+          p4[m] = FULL || key_ok ? x : 0.f;
           pr[4 * g + m] = p4[m];
         }
         *reinterpret_cast<lds_f32x4*>(xb + qt * 4096 + g * 1024) = p4;
@@ -489,8 +493,9 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
     }
   };
   // Phase 2: dV^T += dO^T P (P-wave) or dS and dK^T += Q^T dS (dS-wave).
-  auto phase2 = [&](const lds_u8* slot) {
-    if (pwave) {
+  auto phase2 = [&](auto role, auto full, const lds_u8* slot) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full)::value;
+    if constexpr (decltype(role)::value) {
       const lds_u8* dd = slot + kHalfBytes;
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt)
@@ -513,7 +518,7 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           const float x = p4[m] * (sd[qt][4 * g + m] - d4[m]);
-          dsv[4 * g + m] = key_ok ? x : 0.f;
+          dsv[4 * g + m] = FULL || key_ok ? x : 0.f;
         }
       }
       u32x4 sk[2];
@@ -532,23 +537,40 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
   // Step u: loads of step u landed and the other slot and the P buffer are
   // free (barrier 1); phase 1; P visible to the partner wave (LDS writes
   // done, barrier 2); phase 2. Both barriers are reached by every wave.
-  auto run = [&](int u, lds_u8* cur, lds_u8* nxt) {
+  // The two roles run separate copies of the loop (same barriers), so each
+  // copy's registers hold only its own role's values; whole key tiles take
+  // copies without the key mask.
+  auto run = [&](auto role, auto full, int u, lds_u8* cur, lds_u8* nxt) __attribute__((always_inline)) {
     VEDA_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (u + 1 < n_steps) load_step(u + 1, nxt);
-    if (live) phase1(cur);
+    if (live) phase1(role, full, cur);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's P stores are in LDS
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (live) phase2(cur);
+    if (live) phase2(role, full, cur);
   };
-  if (n_steps > 0) load_step(0, s0);
-  for (int u = 0; u < n_steps; u += 2) {
-    run(u, s0, s1);
-    if (u + 1 >= n_steps) break;
-    run(u + 1, s1, s0);
+  auto loop = [&](auto role, auto full) __attribute__((always_inline)) {
+    if (n_steps > 0) load_step(0, s0);
+    for (int u = 0; u < n_steps; u += 2) {
+      run(role, full, u, s0, s1);
+      if (u + 1 >= n_steps) break;
+      run(role, full, u + 1, s1, s0);
+    }
+  };
+  // a whole key tile (the common case) needs no key mask
+  if (vc == kTile) {
+    if (pwave)
+      loop(std::true_type{}, std::true_type{});
+    else
+      loop(std::false_type{}, std::true_type{});
+  } else {
+    if (pwave)
+      loop(std::true_type{}, std::false_type{});
+    else
+      loop(std::false_type{}, std::false_type{});
   }
 
   uint16_t* orow = pwave ? p.dv + krow * p.dvs + head * p.dvh : p.dk + krow * p.dks + head * p.dkh;
