@@ -326,8 +326,13 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const float pr = __builtin_amdgcn_exp2f(fmaf(st[e], c, -lse2));
-      const float x = pr * (dp[e] - dq_d);
-      ds[e] = (lim < 32 && 8 * (e >> 2) + 4 * hi + (e & 3) >= lim) ? 0.f : x;
+      ds[e] = pr * (dp[e] - dq_d);
+    }
+    if (lim < 32) {  // wave-uniform: only the ragged end of a partial tile
+      const int l = lim - 4 * hi;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (8 * (e >> 2) + (e & 3) >= l) ds[e] = 0.f;
     }
     u32x4 pk[2];
     pack_b(ds, pk);
