@@ -9,8 +9,9 @@
 //                     units (+inf for a row with no key, so its P is 0) and
 //                     D = rowsum(dO * O) - dLSE in fp32 (the LSE output's
 //                     gradient adds dLSE * P to dS), stored as a 1 KB record
-//                     [lse2 x 64 | D x 64 | 0 x 128] that one wave loads
-//                     into LDS with one DMA.
+//                     [lse2 x 64 | -D x 64 | 0 x 128] that one wave loads
+//                     into LDS with one DMA. -D is the initial accumulator
+//                     of the dP products, so they produce dP - D directly.
 //   dq_kernel         workgroup = (head, query tile), walking the forward
 //                     block lists (the key tiles of the row).
 //   dkv_kernel        workgroup = (head, key tile), walking the transposed
@@ -225,7 +226,7 @@ __global__ void __launch_bounds__(256) bwd_stats_kernel(BwdParams p) {
     if (sub == 0) {
       const float l = p.lse[head * p.lse_sh + row * p.lse_ss];
       out[rr] = l == -INFINITY ? INFINITY : l * kLog2e;
-      out[64 + rr] = p.dlse != nullptr ? acc - p.dlse[head * p.dlse_sh + row * p.dlse_ss] : acc;
+      out[64 + rr] = p.dlse != nullptr ? p.dlse[head * p.dlse_sh + row * p.dlse_ss] - acc : -acc;
     }
   }
   if (tid < 128) out[128 + tid] = 0.f;
@@ -275,7 +276,13 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
   }
   const float* rec = p.stats + (head * 2 * p.n_q_tiles + 2 * r + (wave >> 1)) * kRecFloats;
   const float lse2 = rec[(32 * wave + li) & 63];
-  const float dq_d = rec[64 + ((32 * wave + li) & 63)];
+  // -D of this lane's row, the initial accumulator of its dP products
+  f32x16 neg_d;
+  {
+    const float nd = rec[64 + ((32 * wave + li) & 63)];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) neg_d[e] = nd;
+  }
   f32x16 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -310,12 +317,9 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
   auto half_step = [&](const lds_u8* slot, int kh, int lim) {
     const lds_u8* ks = slot + kh * 32 * 256;
     const lds_u8* vs = slot + kHalfBytes + kh * 32 * 256;
-    f32x16 st, dp;
+    f32x16 st, dp = neg_d;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      st[e] = 0.f;
-      dp[e] = 0.f;
-    }
+    for (int e = 0; e < 16; ++e) st[e] = 0.f;
 #pragma unroll
     for (int s = 0; s < 8; ++s)
       st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(ks + f.row[s])), qf[s], st, 0, 0, 0);
@@ -326,7 +330,7 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const float pr = __builtin_amdgcn_exp2f(fmaf(st[e], c, -lse2));
-      ds[e] = pr * (dp[e] - dq_d);
+      ds[e] = pr * dp[e];  // dp holds dP - D
     }
     if (lim < 32) {  // wave-uniform: only the ragged end of a partial tile
       const int l = lim - 4 * hi;
@@ -470,8 +474,19 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
     const lds_u8* a = P ? slot : slot + kHalfBytes;  // Q or dO rows
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
+      if constexpr (P) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sd[qt][e] = 0.f;
+        for (int e = 0; e < 16; ++e) sd[qt][e] = 0.f;
+      } else {
+        // dP products start from -D of the step's rows: they give dP - D
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 d4 =
+              *reinterpret_cast<const lds_f32x4*>(slot + kSlot + 256 + 4 * (32 * qt + 8 * g + 4 * hi));
+#pragma unroll
+          for (int m = 0; m < 4; ++m) sd[qt][4 * g + m] = d4[m];
+        }
+      }
 #pragma unroll
       for (int s = 0; s < 8; ++s)
         sd[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(a + qt * 8192 + f.row[s])),
@@ -512,17 +527,15 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
                 tr_frag(dd + qt * 8192, f, dt, kk), as_bf16x8(pk[qt][kk]), acc[dt], 0, 0, 0);
       return;
     }
-    const lds_u8* sr = slot + kSlot;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       float dsv[16];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const f32x4 d4 = *reinterpret_cast<const lds_f32x4*>(sr + 256 + 4 * (32 * qt + 8 * g + 4 * hi));
         const f32x4 p4 = *reinterpret_cast<const lds_f32x4*>(xb + qt * 4096 + g * 1024);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const float x = p4[m] * (sd[qt][4 * g + m] - d4[m]);
+          const float x = p4[m] * sd[qt][4 * g + m];  // sd holds dP - D
           dsv[4 * g + m] = FULL || key_ok ? x : 0.f;
         }
       }
