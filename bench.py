@@ -396,10 +396,14 @@ def main() -> int:
         return _backward(c, kept, args.steps, args.warmup)
     flop = 4.0 * 128 * 128 * D * kept
     # What the kernel executes: the valid keys of every kept block (padding
-    # rows of partial key tiles are neither loaded nor multiplied); query
-    # rows all count.
-    valid_keys = float((c['mask'].float() * lay.valid_count.float()[None, None, :]).sum())
-    exec_flop = 4.0 * 128 * D * valid_keys
+    # rows of partial key tiles are neither loaded nor multiplied), for all
+    # 128 query rows in the P.V products and for the 32-row groups that hold
+    # a real row in the Q.K^T products (a group of padding rows, all zero,
+    # skips them).
+    vc = lay.valid_count.float()
+    keys_per_row = (c['mask'].float() * vc[None, None, :]).sum(-1)          # [H, R]
+    live_groups = torch.ceil(vc[:keys_per_row.shape[1]] / 32.0)             # per query tile
+    exec_flop = float((keys_per_row * (2.0 * 128 * D + 2.0 * 32 * D * live_groups[None, :])).sum())
     dense_flop = 4.0 * c['used'] * c['used'] * HEADS * D
 
     def step():

@@ -35,6 +35,8 @@
 //      (i mod 4) of source lane 4 j + i / 4, j = 0..3), are conflict-free.
 // The pipeline over the kept blocks is described at the half-block section.
 
+#include <type_traits>
+
 #include "veda_common.h"
 #include "veda_pipeline.h"
 
@@ -657,6 +659,43 @@ __device__ __forceinline__ void sstep(const lds_u8* slot, const HFrag& fa, const
   sub_pv(slot, fb, kb, w);
 }
 
+// The step of a wave whose 32 query rows are all zero (the padding rows of
+// a partial query tile, whose gathered q is zero): every valid key scores
+// exactly 0, so P is 1 on the valid keys and 0 on the masked ones, the
+// running max is 0 from the first valid key on and the row sum counts the
+// valid keys. Only the P.V products remain; the result is bit-identical to
+// sstep's on the same rows (the same products of the same exact P).
+__device__ __forceinline__ void sstep_zero_q(const lds_u8* slot, const HFrag& fa,
+                                             const HFrag& fb, int la, int lb, int hi,
+                                             WaveState& w) {
+  if (la <= 0 && lb <= 0) return;  // no valid key: P is 0 everywhere
+  w.m_run = 0.f;
+  auto probs = [&](int lim, u32x4 (&pk)[2]) {
+    if (lim >= 32) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) pk[kk] = u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+      w.l_run += 16.f;
+      return;
+    }
+    // register e holds key 8 (e / 4) + 4 hi + e % 4 of the sub-block
+    float ps[16];
+    int n = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const bool v = 8 * (e >> 2) + 4 * hi + (e & 3) < lim;
+      ps[e] = v ? 1.f : 0.f;
+      n += v;
+    }
+    w.l_run += (float)n;
+    pack_probs(ps, pk);
+  };
+  u32x4 ka[2], kb[2];
+  probs(la, ka);
+  probs(lb, kb);
+  sub_pv(slot, fa, ka, w);
+  sub_pv(slot, fb, kb, w);
+}
+
 // One 32-key sub-block of a compensation step (the virtual keys of key
 // tiles key0 .. key0 + 31): p = exp2(s c - ref2) where the tile's weight
 // (its real row count if dropped, else 0) is positive, den += p * weight,
@@ -861,6 +900,18 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     w.qf[s] = q_live ? as_bf16x8(ld16(qptr + 16 * s + 8 * hi)) : as_bf16x8(u32x4{0, 0, 0, 0});
 #pragma unroll
   for (int s = 0; s < 8; ++s) asm volatile("" : : "v"(w.qf[s]));
+  // a wave whose 32 query rows are all zero (padding rows) takes the
+  // product-free step (wave-uniform)
+  bool q_zero = false;
+  if (MODE == kSparse) {
+    uint32_t any = 0;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const u32x4 x = __builtin_bit_cast(u32x4, w.qf[s]);
+      any |= x[0] | x[1] | x[2] | x[3];
+    }
+    q_zero = __ballot(any != 0) == 0;
+  }
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -1072,32 +1123,44 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
         dma16(vb, live ? dma.v[u4] : dma.v_skip[u4], slot + kHalfBytes + seg * 1024);
       }
     };
-    auto compute = [&](uint32_t ra, uint32_t rb, const lds_u8* cur) {
-      sstep(cur, fa, fb, c, (int)(ra & 63u), (int)(rb & 63u), hi, w);
+    auto compute = [&](auto zero, uint32_t ra, uint32_t rb, const lds_u8* cur)
+                       __attribute__((always_inline)) {
+      if constexpr (decltype(zero)::value)
+        sstep_zero_q(cur, fa, fb, (int)(ra & 63u), (int)(rb & 63u), hi, w);
+      else
+        sstep(cur, fa, fb, c, (int)(ra & 63u), (int)(rb & 63u), hi, w);
     };
-    uint32_t ca = 0, cb = 0;
-    if (n_steps > 0) {
-      fetch(0, ca, cb);
-      load_rec(ca, cb, s0);
-    }
-    for (int u = 0; u < n_steps; u += 2) {
-      uint32_t na = 0, nb = 0;
-      VEDA_WAIT_VM(0);
-      __builtin_amdgcn_s_barrier();
-      if (u + 1 < n_steps) {
-        fetch(u + 1, na, nb);
-        load_rec(na, nb, s1);
-      }
-      compute(ca, cb, s0);
-      if (u + 1 >= n_steps) break;
-      VEDA_WAIT_VM(0);
-      __builtin_amdgcn_s_barrier();
-      if (u + 2 < n_steps) {
-        fetch(u + 2, ca, cb);
+    // Two copies of the loop, one per kind of wave (same loads and
+    // barriers), so each keeps O in one set of registers.
+    auto walk = [&](auto zero) __attribute__((always_inline)) {
+      uint32_t ca = 0, cb = 0;
+      if (n_steps > 0) {
+        fetch(0, ca, cb);
         load_rec(ca, cb, s0);
       }
-      compute(na, nb, s1);
-    }
+      for (int u = 0; u < n_steps; u += 2) {
+        uint32_t na = 0, nb = 0;
+        VEDA_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        if (u + 1 < n_steps) {
+          fetch(u + 1, na, nb);
+          load_rec(na, nb, s1);
+        }
+        compute(zero, ca, cb, s0);
+        if (u + 1 >= n_steps) break;
+        VEDA_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        if (u + 2 < n_steps) {
+          fetch(u + 2, ca, cb);
+          load_rec(ca, cb, s0);
+        }
+        compute(zero, na, nb, s1);
+      }
+    };
+    if (q_zero)
+      walk(std::true_type{});
+    else
+      walk(std::false_type{});
   } else {
   if (n_steps > 0) load_step(0, s0);
   if (!VKEYS) {
