@@ -82,6 +82,25 @@ def test_empty_query_tiles_give_zero_and_neg_inf_lse():
     _close(lse.T, ref_lse.T, real)
 
 
+def test_all_zero_query_groups_match_the_oracle_on_every_row():
+    """Query rows in 32-row groups that are all zero take the kernel's
+    product-free step (padding rows of partial tiles, and here also a whole
+    group of real rows zeroed): every row, padding included, against the
+    oracle (the uniform average of the valid kept keys, LSE = log of their
+    count), with an empty row and a tile whose groups are mixed."""
+    lay, olay, qt, kt, vt, mask = _case(helpers.small_layout(), seed=7)
+    assert olay.partial_tiles.numel() > 0
+    qt = qt.clone()
+    qt[2 * 128 + 32:2 * 128 + 64] = 0           # one whole group of real rows
+    qt[3 * 128 + 40:3 * 128 + 64] = 0           # part of a group: stays on the full step
+    mask[0, 5] = False                          # a query tile with no key at all
+    out, lse = kernels.block_sparse_attention(qt.cuda(), kt.cuda(), vt.cuda(), mask.cuda(), lay,
+                                              return_lse=True)
+    ref, ref_lse = oa.block_sparse_attention(qt, kt, vt, mask, olay.valid_count, return_lse=True)
+    _close(out, ref)
+    _close(lse.T, ref_lse.T)
+
+
 def test_query_tile_subset_rows():
     """q holds only some query tiles; mask rows follow q (fa4.py:308-313)."""
     lay, olay, qt, kt, vt, mask = _case(helpers.small_layout(), seed=3)
