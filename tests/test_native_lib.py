@@ -6,6 +6,7 @@ they run without a GPU)."""
 import ctypes
 import pathlib
 import re
+import threading
 
 import pytest
 
@@ -102,3 +103,35 @@ def test_supports_refuses_cpu_tensors_and_unknown_ops():
         assert not kernels.supports(x, op)
     with pytest.raises(ValueError, match='op must be'):
         kernels.supports(x, 'dense')
+
+
+def test_error_messages_are_per_thread():
+    """The library keeps no host state shared between calls; a failed call's
+    message is the calling thread's own (threads that each drive a GPU need
+    no lock around the calls). Two threads fail different entry points
+    thousands of times and each always reads its own message."""
+    lib = _native.load()
+    failures = []
+
+    def heat():
+        for _ in range(3000):
+            rc = lib.veda_block_heat(None, 0, 0, None, 0, 0, None, 0, 0, None, None, 1, 1,
+                                     1, 128, 3, 1.0, None, None)
+            msg = lib.veda_last_error().decode()
+            if rc != -1 or 'reduce' not in msg:
+                failures.append(('heat', rc, msg))
+
+    def gather():
+        for _ in range(3000):
+            rc = lib.veda_gather_tiles(None, 0, 0, 0, 0, None, None, None, 1, None, 1, 96,
+                                       None, 0, 0, None, None, None, None)
+            msg = lib.veda_last_error().decode()
+            if rc != -1 or 'head_dim' not in msg:
+                failures.append(('gather', rc, msg))
+
+    threads = [threading.Thread(target=f) for f in (heat, gather)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not failures, failures[:3]
