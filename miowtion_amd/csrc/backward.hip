@@ -409,7 +409,14 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
   int64_t head, j;
   front_first(blockIdx.x, p.n_heads, p.n_k_tiles, p.front, head, j);
   const int vc = __builtin_amdgcn_readfirstlane(clamp_vc(p.valid_count[j]));
-  const int64_t krow = j * kTile + 32 * kg + li;
+  // A key tile with at most 32 valid keys has one live key group; the pairs
+  // of groups 0 and 1 then split the step's two 32-row halves of it between
+  // them (each pair one half, partial sums added at the end), so two SIMDs
+  // work instead of one.
+  const bool split = vc <= 32;
+  const int kgl = split ? 0 : kg;                      // the key group this pair computes
+  const int64_t krow = j * kTile + 32 * kg + li;       // the rows this wave writes
+  const int64_t kcomp = j * kTile + 32 * kgl + li;     // the key this lane computes for
   const int nq = (int)p.n_q_tiles;
 
   if (wave == 0) {
@@ -423,7 +430,7 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
   }
 
   // B operand rows: K (P-wave) or V (dS-wave) of this lane's key
-  const uint16_t* brow = pwave ? p.k + krow * p.ks + head * p.kh : p.v + krow * p.vs + head * p.vh;
+  const uint16_t* brow = pwave ? p.k + kcomp * p.ks + head * p.kh : p.v + kcomp * p.vs + head * p.vh;
   bf16x8 bf[8];
 #pragma unroll
   for (int s = 0; s < 8; ++s) bf[s] = as_bf16x8(ld16(brow + 16 * s + 8 * hi));
@@ -445,8 +452,8 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
   }
   const Frag f = frag_offsets(lane);
   const float c = p.scale_log2;
-  const bool key_ok = 32 * kg + li < vc;
-  const bool live = 32 * kg < vc;
+  const bool key_ok = 32 * kgl + li < vc;
+  const bool live = split ? kg < 2 : 32 * kg < vc;
   lds_u8* xb = (lds_u8*)xbuf + kg * 2 * 4096 + lane * 16;  // + qt * 4096 + e4 * 1024
 
   auto load_step = [&](int u, lds_u8* slot) {
@@ -468,15 +475,19 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
   // Phase 1: S and P (P-wave) or dP (dS-wave) of both 32-row halves.
   f32x16 sd[2];
   u32x4 pk[2][2];
-  auto phase1 = [&](auto role, auto full, const lds_u8* slot) __attribute__((always_inline)) {
+  auto phase1 = [&](auto role, auto full, auto halves, const lds_u8* slot)
+                    __attribute__((always_inline)) {
     constexpr bool P = decltype(role)::value;
     constexpr bool FULL = decltype(full)::value;  // every key of the tile valid
+    constexpr int NQT = decltype(halves)::value;  // 32-row halves this pair computes
+    const int qt0 = NQT == 2 ? 0 : kg;
     const lds_u8* a = P ? slot : slot + kHalfBytes;  // Q or dO rows
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int i = 0; i < NQT; ++i) {
+      const int qt = qt0 + i;
       if constexpr (P) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sd[qt][e] = 0.f;
+        for (int e = 0; e < 16; ++e) sd[i][e] = 0.f;
       } else {
         // dP products start from -D of the step's rows: they give dP - D
 #pragma unroll
@@ -484,18 +495,19 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
           const f32x4 d4 =
               *reinterpret_cast<const lds_f32x4*>(slot + kSlot + 256 + 4 * (32 * qt + 8 * g + 4 * hi));
 #pragma unroll
-          for (int m = 0; m < 4; ++m) sd[qt][4 * g + m] = d4[m];
+          for (int m = 0; m < 4; ++m) sd[i][4 * g + m] = d4[m];
         }
       }
 #pragma unroll
       for (int s = 0; s < 8; ++s)
-        sd[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(a + qt * 8192 + f.row[s])),
-                                                         bf[s], sd[qt], 0, 0, 0);
+        sd[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(a + qt * 8192 + f.row[s])),
+                                                        bf[s], sd[i], 0, 0, 0);
     }
     if constexpr (!P) return;
     const lds_u8* sr = slot + kSlot;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int i = 0; i < NQT; ++i) {
+      const int qt = qt0 + i;
       float pr[16];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -503,39 +515,43 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
         f32x4 p4;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const float x = __builtin_amdgcn_exp2f(fmaf(sd[qt][4 * g + m], c, -l4[m]));
+          const float x = __builtin_amdgcn_exp2f(fmaf(sd[i][4 * g + m], c, -l4[m]));
           p4[m] = FULL || key_ok ? x : 0.f;
           pr[4 * g + m] = p4[m];
         }
         *reinterpret_cast<lds_f32x4*>(xb + qt * 4096 + g * 1024) = p4;
       }
-      pack_b(pr, pk[qt]);
+      pack_b(pr, pk[i]);
     }
   };
   // Phase 2: dV^T += dO^T P (P-wave) or dS and dK^T += Q^T dS (dS-wave).
-  auto phase2 = [&](auto role, auto full, const lds_u8* slot) __attribute__((always_inline)) {
+  auto phase2 = [&](auto role, auto full, auto halves, const lds_u8* slot)
+                    __attribute__((always_inline)) {
     constexpr bool FULL = decltype(full)::value;
+    constexpr int NQT = decltype(halves)::value;
+    const int qt0 = NQT == 2 ? 0 : kg;
     if constexpr (decltype(role)::value) {
       const lds_u8* dd = slot + kHalfBytes;
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
+      for (int i = 0; i < NQT; ++i)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
           for (int dt = 0; dt < 4; ++dt)
             acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                tr_frag(dd + qt * 8192, f, dt, kk), as_bf16x8(pk[qt][kk]), acc[dt], 0, 0, 0);
+                tr_frag(dd + (qt0 + i) * 8192, f, dt, kk), as_bf16x8(pk[i][kk]), acc[dt], 0, 0, 0);
       return;
     }
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int i = 0; i < NQT; ++i) {
+      const int qt = qt0 + i;
       float dsv[16];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const f32x4 p4 = *reinterpret_cast<const lds_f32x4*>(xb + qt * 4096 + g * 1024);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const float x = p4[m] * sd[qt][4 * g + m];  // sd holds dP - D
+          const float x = p4[m] * sd[i][4 * g + m];  // sd holds dP - D
           dsv[4 * g + m] = FULL || key_ok ? x : 0.f;
         }
       }
@@ -558,37 +574,73 @@ __global__ void __launch_bounds__(kDkvThreads) dkv_kernel(BwdParams p) {
   // The two roles run separate copies of the loop (same barriers), so each
   // copy's registers hold only its own role's values; whole key tiles take
   // copies without the key mask.
-  auto run = [&](auto role, auto full, int u, lds_u8* cur, lds_u8* nxt) __attribute__((always_inline)) {
+  auto run = [&](auto role, auto full, auto halves, int u, lds_u8* cur, lds_u8* nxt)
+                 __attribute__((always_inline)) {
     VEDA_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (u + 1 < n_steps) load_step(u + 1, nxt);
-    if (live) phase1(role, full, cur);
+    if (live) phase1(role, full, halves, cur);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's P stores are in LDS
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (live) phase2(role, full, cur);
+    if (live) phase2(role, full, halves, cur);
   };
-  auto loop = [&](auto role, auto full) __attribute__((always_inline)) {
+  auto loop = [&](auto role, auto full, auto halves) __attribute__((always_inline)) {
     if (n_steps > 0) load_step(0, s0);
     for (int u = 0; u < n_steps; u += 2) {
-      run(role, full, u, s0, s1);
+      run(role, full, halves, u, s0, s1);
       if (u + 1 >= n_steps) break;
-      run(role, full, u + 1, s1, s0);
+      run(role, full, halves, u + 1, s1, s0);
     }
   };
+  using Two = std::integral_constant<int, 2>;
+  using One = std::integral_constant<int, 1>;
   // a whole key tile (the common case) needs no key mask
   if (vc == kTile) {
     if (pwave)
-      loop(std::true_type{}, std::true_type{});
+      loop(std::true_type{}, std::true_type{}, Two{});
     else
-      loop(std::false_type{}, std::true_type{});
+      loop(std::false_type{}, std::true_type{}, Two{});
+  } else if (!split) {
+    if (pwave)
+      loop(std::true_type{}, std::false_type{}, Two{});
+    else
+      loop(std::false_type{}, std::false_type{}, Two{});
   } else {
     if (pwave)
-      loop(std::true_type{}, std::false_type{});
+      loop(std::true_type{}, std::false_type{}, One{});
     else
-      loop(std::false_type{}, std::false_type{});
+      loop(std::false_type{}, std::false_type{}, One{});
+  }
+  if (split) {
+    // pair 1 hands its half's partial sums to pair 0 through the ring (free
+    // now), then writes its own rows, padding keys, as zeros
+    __syncthreads();
+    lds_f32x4* red = reinterpret_cast<lds_f32x4*>(s0) + (pwave ? 0 : 16 * 64) + lane;
+    if (kg == 1) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          red[(4 * dt + g) * 64] = f32x4{acc[dt][4 * g], acc[dt][4 * g + 1], acc[dt][4 * g + 2],
+                                         acc[dt][4 * g + 3]};
+#pragma unroll
+          for (int m = 0; m < 4; ++m) acc[dt][4 * g + m] = 0.f;
+        }
+    }
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 o = red[(4 * dt + g) * 64];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) acc[dt][4 * g + m] += o[m];
+        }
+    }
   }
 
   uint16_t* orow = pwave ? p.dv + krow * p.dvs + head * p.dvh : p.dk + krow * p.dks + head * p.dkh;
