@@ -568,8 +568,18 @@ __device__ __forceinline__ SDma sdma_offsets(int64_t ks, int64_t vs, int wave, i
   return d;
 }
 
-// Scores of one 32-key sub-block, masked past `lim` keys of it (lim >= 32:
-// none; lim <= 0: all).
+// Scores of a 32-key sub-block past its first `lim` keys set to -inf (lim >=
+// 32: none; lim <= 0: all); register e holds key 8 (e / 4) + 4 hi + e % 4.
+__device__ __forceinline__ void mask_scores(f32x16& s, int lim, int hi) {
+  if (lim < 32) {
+    const int l = lim - 4 * hi;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (8 * (e >> 2) + (e & 3) >= l) s[e] = -INFINITY;
+  }
+}
+
+// Scores of one 32-key sub-block, masked past `lim` keys of it.
 __device__ __forceinline__ f32x16 sub_scores(const lds_u8* slot, const HFrag& f,
                                              const WaveState& w, int lim, int hi) {
   u32x4 kf[8];
@@ -582,13 +592,36 @@ __device__ __forceinline__ f32x16 sub_scores(const lds_u8* slot, const HFrag& f,
 #pragma unroll
   for (int k = 0; k < 8; ++k)
     s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[k]), w.qf[k], s, 0, 0, 0);
-  if (lim < 32) {
-    const int l = lim - 4 * hi;
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      if (8 * (e >> 2) + (e & 3) >= l) s[e] = -INFINITY;
-  }
+  mask_scores(s, lim, hi);
   return s;
+}
+
+// Scores of both 32-key sub-blocks of a step, as two interleaved MFMA
+// chains (each fragment read has the other chain's product to hide behind),
+// then the masks of sub-blocks with fewer than 32 valid keys.
+__device__ __forceinline__ void pair_scores(const lds_u8* slot, const HFrag& fa, const HFrag& fb,
+                                            const WaveState& w, int la, int lb, int hi,
+                                            f32x16& sa, f32x16& sb) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sa[e] = sb[e] = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const u32x4 ka = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(slot + fa.k[k]);
+    const u32x4 kb = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(slot + fb.k[k]);
+    sa = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka), w.qf[k], sa, 0, 0, 0);
+    sb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kb), w.qf[k], sb, 0, 0, 0);
+  }
+  // issue order: the reads of k + 2 before the products of k (more reads
+  // ahead than the compiler's own schedule keeps; all 16 ahead was slower)
+  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  mask_scores(sa, la, hi);
+  mask_scores(sb, lb, hi);
 }
 
 __device__ __forceinline__ void sub_pv(const lds_u8* slot, const HFrag& f, const u32x4 (&pk)[2],
@@ -621,8 +654,8 @@ __device__ __forceinline__ void pack_probs(const float (&ps)[16], u32x4 (&pk)[2]
 // sub-block b makes the compiler move O between register sets every step).
 __device__ __forceinline__ void sstep(const lds_u8* slot, const HFrag& fa, const HFrag& fb,
                                       float c, int la, int lb, int hi, WaveState& w) {
-  const f32x16 sa = sub_scores(slot, fa, w, la, hi);
-  const f32x16 sb = sub_scores(slot, fb, w, lb, hi);
+  f32x16 sa, sb;
+  pair_scores(slot, fa, fb, w, la, lb, hi, sa, sb);
   float mloc = -INFINITY;
 #pragma unroll
   for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sa[e]);
