@@ -304,8 +304,8 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
   const Frag f = frag_offsets(lane);
   const float c = p.scale_log2;
 
-  auto load_step = [&](int u, lds_u8* slot) {
-    const int t = __builtin_amdgcn_readfirstlane(steps[u]);
+  // the step list entry t of a step: (key tile << 1 | half)
+  auto load_step = [&](int t, lds_u8* slot) {
     const int64_t row0 = (int64_t)(t >> 1) * kTile + (t & 1) * kHalf;
     const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
     const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
@@ -315,6 +315,7 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
       dma16(vb, voff[s], slot + kHalfBytes + (4 * wave + s) * 1024);
     }
   };
+  auto entry = [&](int u) { return __builtin_amdgcn_readfirstlane((int)steps[u]); };
   // One 32-key half kh of a step with `lim` valid keys in it (lim >= 32: all).
   auto half_step = [&](const lds_u8* slot, int kh, int lim) {
     const lds_u8* ks = slot + kh * 32 * 256;
@@ -322,12 +323,22 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
     f32x16 st, dp = neg_d;
 #pragma unroll
     for (int e = 0; e < 16; ++e) st[e] = 0.f;
+    // S^T and dP^T as two interleaved chains, the reads of k-step s + 2
+    // issued before the products of s
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(ks + f.row[s])), qf[s], st, 0, 0, 0);
+    for (int s = 0; s < 8; ++s) {
+      const u32x4 ka = lds16(ks + f.row[s]);
+      const u32x4 va = lds16(vs + f.row[s]);
+      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka), qf[s], st, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(va), dof[s], dp, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(lds16(vs + f.row[s])), dof[s], dp, 0, 0, 0);
+    for (int s = 0; s < 6; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     float ds[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -349,27 +360,30 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag(ks, f, dt, kk), as_bf16x8(pk[kk]),
                                                           acc[dt], 0, 0, 0);
   };
-  auto compute = [&](int u, const lds_u8* slot) {
-    const int t = __builtin_amdgcn_readfirstlane(steps[u]);
-    const int vc = __builtin_amdgcn_readfirstlane((int)tvc[t >> 1]);
-    const int vch = t & 1 ? vc - kHalf : min(vc, kHalf);  // valid keys of the step
+  auto compute = [&](int vch, const lds_u8* slot) {
     half_step(slot, 0, vch);
     if (vch > 32) half_step(slot, 1, vch - 32);
   };
 
   lds_u8* s0 = (lds_u8*)ring[0];
   lds_u8* s1 = (lds_u8*)ring[1];
-  // Step u: wait for this wave's loads (the only ones in flight), barrier
+  // Step u: read the step list (written before the loop) for steps u and
+  // u + 1, wait for this wave's loads (the only ones in flight), barrier
   // (every wave's loads of step u are in LDS and every wave is done reading
   // the other slot), issue step u + 1 into the other slot, compute step u.
+  // The list reads stay above the barrier, out of the products' schedule.
   auto run = [&](int u, lds_u8* cur, lds_u8* nxt) {
+    const int t = entry(u);
+    const int vc = __builtin_amdgcn_readfirstlane((int)tvc[t >> 1]);
+    const int vch = t & 1 ? vc - kHalf : min(vc, kHalf);  // valid keys of the step
+    const int tn = u + 1 < n_steps ? entry(u + 1) : 0;
     VEDA_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");  // no LDS read of step u above the barrier
-    if (u + 1 < n_steps) load_step(u + 1, nxt);
-    compute(u, cur);
+    if (u + 1 < n_steps) load_step(tn, nxt);
+    compute(vch, cur);
   };
-  if (n_steps > 0) load_step(0, s0);
+  if (n_steps > 0) load_step(entry(0), s0);
   for (int u = 0; u < n_steps; u += 2) {
     run(u, s0, s1);
     if (u + 1 >= n_steps) break;
