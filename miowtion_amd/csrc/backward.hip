@@ -527,11 +527,12 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
       const lds_u8* qs = slot;
       const lds_u8* ds = slot + kHalfBytes;
       const lds_u8* rec = slot + kSlot;
-      f32x4 s[NQB], dp[NQB];
+      f32x4 s[NQB], dp[NQB], lse[NQB];
 #pragma unroll
       for (int i = 0; i < NQB; ++i) {
         s[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         dp[i] = *reinterpret_cast<const lds_f32x4*>(rec + 256 + roff + 64 * i);  // -D
+        lse[i] = *reinterpret_cast<const lds_f32x4*>(rec + roff + 64 * i);
       }
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc)
@@ -543,10 +544,19 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
 #pragma unroll
         for (int i = 0; i < NQB; ++i)
           dp[i] = mfma16(lds16(ds + i * 4096 + arow[cc]), vf[cc], dp[i]);
+      // issue order: the record reads, then each row read four products
+      // ahead of its product
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * NQB + 4, 0);
+#pragma unroll
+      for (int x = 0; x < 8 * NQB - 4; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
       uint32_t pp[NQB][2], pd[NQB][2];
 #pragma unroll
       for (int i = 0; i < NQB; ++i) {
-        const f32x4 l4 = *reinterpret_cast<const lds_f32x4*>(rec + roff + 64 * i);
+        const f32x4 l4 = lse[i];
         float pr[4], dv[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -587,6 +597,15 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
                                                                      (lds_i16x4*)(qa + 4096)));
           acc_k[db] = mfma16(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, bd, acc_k[db]);
         }
+        // issue order: the reads of head-dim block db + 1 before the products of db
+        constexpr int R = NQB == 1 ? 2 : 4;
+        __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
+#pragma unroll
+        for (int db = 1; db < 8; ++db) {
+          __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
       }
     };
     // Step u: wait for this wave's loads (the only ones in flight), barrier
