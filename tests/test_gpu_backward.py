@@ -175,6 +175,32 @@ def test_config2_two_heads():
         _bar(a, w, name)
 
 
+def test_every_key_tile_form():
+    """Key tiles with 128, 72, 40 and 16 valid keys take the dK/dV kernel's
+    three forms (8 key groups of 16 x 4 query blocks; 4 x 2; 2 x 1) with a
+    partly valid key group in each and a key group with no valid key in the
+    last: every gradient row against the per-tile oracle."""
+    spans = [(0, (2, 8, 21)), (336, (2, 8, 25)), (736, (3, 8, 18))]
+    used = 736 + 3 * 8 * 18
+    lay = helpers.product_layout(spans, used, used, '1x8x16', device='cuda')
+    olay = helpers.oracle_layout(spans, used, used, '1x8x16')
+    assert sorted(set(olay.valid_count.tolist())) == [16, 40, 72, 128]
+    H = 3
+    q, k, v = helpers.qkv(lay.seq_len, H, 128, seed=11)
+    qt, kt, vt = (kernels.gather_tiles(t.cuda(), lay, None) for t in (q, k, v))
+    g = torch.Generator().manual_seed(12)
+    n = lay.n_tiles
+    mask = torch.rand(H, n, n, generator=g) < 0.5
+    mask |= torch.eye(n, dtype=torch.bool)[None]
+    mask &= olay.kv_ok[None, None, :]
+    grad_out = torch.randn(qt.shape, generator=g).to(torch.bfloat16)
+    got = _gpu_grads(qt, kt, vt, mask.cuda(), lay, grad_out.cuda())
+    want = oa.block_sparse_attention_grads_by_tile(qt.cpu(), kt.cpu(), vt.cpu(), mask,
+                                                   olay.valid_count, grad_out.float())
+    for name, a, w in zip('qkv', got, want):
+        _bar(a, w, name)
+
+
 def test_largest_tile_count():
     """2048 tiles a side, one head, a dense row and a dense column (the
     longest forward and transposed lists): every gradient row against the
