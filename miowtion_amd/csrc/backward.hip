@@ -359,6 +359,14 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
       for (int dt = 0; dt < 4; ++dt)
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag(ks, f, dt, kk), as_bf16x8(pk[kk]),
                                                           acc[dt], 0, 0, 0);
+    // issue order: the transposed reads of product i + 2 before product i
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   };
   auto compute = [&](int vch, const lds_u8* slot) {
     half_step(slot, 0, vch);
