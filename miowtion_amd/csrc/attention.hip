@@ -967,6 +967,17 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     const float lk = p.lse_kept[head * p.lk_h + qrow * p.lk_s];
     ref2 = (lk > -INFINITY && lk < INFINITY) ? lk * 1.4426950408889634f : 0.f;
   }
+  if (MODE == kSparse) {
+    // The sparse walk loads no segment past a sub-block's valid keys, so a
+    // slot keeps whatever V rows it held there: zero both V halves once, so
+    // those rows are finite (their probabilities are exactly 0).
+#pragma unroll
+    for (int i = 0; i < 2 * kHalfBytes / (16 * kThreads2); ++i) {
+      const int off = (i * kThreads2 + tid) * 16;
+      lds_u8* dst = (lds_u8*)ring[off / kHalfBytes] + kHalfBytes + off % kHalfBytes;
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(dst) = u32x4{0, 0, 0, 0};
+    }
+  }
   __syncthreads();  // step list, weights, valid counts and list step count ready
   const int n_lsteps = __builtin_amdgcn_readfirstlane(step_total);
   const int n_big = LISTS ? __builtin_amdgcn_readfirstlane(step_big) : 0;
@@ -1150,7 +1161,8 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     };
     // waves 0, 1 load sub-block a, waves 2, 3 sub-block b (rows
     // 16 (wave & 1) .. + 15 of it); a segment past the sub-block's valid
-    // keys reloads its first rows (not read: masked)
+    // keys is not loaded (its rows are masked: the scores become -inf, the
+    // probabilities exactly 0, and the slot's V rows there are finite)
     auto load_rec = [&](uint32_t ra, uint32_t rb, lds_u8* slot) {
       const uint32_t rec = wave < 2 ? ra : rb;
       const int64_t base = (int64_t)(rec >> 6);
@@ -1160,9 +1172,10 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
 #pragma unroll
       for (int u4 = 0; u4 < 4; ++u4) {
         const int seg = 4 * wave + u4;
-        const bool live = 4 * (4 * (wave & 1) + u4) < lim;
-        dma16(kb, live ? dma.k[u4] : dma.k_skip[u4], slot + seg * 1024);
-        dma16(vb, live ? dma.v[u4] : dma.v_skip[u4], slot + kHalfBytes + seg * 1024);
+        if (4 * (4 * (wave & 1) + u4) < lim) {
+          dma16(kb, dma.k[u4], slot + seg * 1024);
+          dma16(vb, dma.v[u4], slot + kHalfBytes + seg * 1024);
+        }
       }
     };
     auto compute = [&](auto zero, uint32_t ra, uint32_t rb, const lds_u8* cur)
