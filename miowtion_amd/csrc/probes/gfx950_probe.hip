@@ -5,6 +5,9 @@
 //                        overlap across two waves of a SIMD and inside one
 //   gfx950_probe lanes   512 single-wave dispatches for the LDS lane-group
 //                        study (run under rocprofv3 by lds_lanes.py)
+//   gfx950_probe dma     global -> LDS load rate per CU from an L2-resident
+//                        buffer: global_load_lds_dwordx4 against plain
+//                        global_load_dwordx4 (and with a ds_write_b128)
 //
 // Every access stays inside the kernel's own LDS array or its output
 // buffer; every loop has a fixed trip count.
@@ -239,6 +242,61 @@ __global__ void __launch_bounds__(64) lane_kernel(uint32_t* out, int a, int b) {
 
 constexpr int kLaneA[4] = {0, 5, 17, 42};
 
+// ---------------------------------------------------------------------------
+// Load rate into a CU: WAVES waves per workgroup, one workgroup per CU (64 KB
+// of LDS), each wave kDmaBatches batches of 8 loads of 1 KB (64 lanes x 16 B)
+// from a 1 MB buffer (L2-resident after the first pass), then a wait for
+// all of them, as the sparse forward waits per step.
+//   0: global_load_lds_dwordx4 into the wave's 8 KB of LDS
+//   1: global_load_dwordx4 into registers
+//   2: global_load_dwordx4 into registers, then ds_write_b128 of each
+constexpr int kDmaBatches = 512;
+constexpr uint32_t kDmaBufBytes = 1u << 20;
+
+template <int MODE, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) dma_kernel(const char* src, uint32_t* out) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[WAVES * 8192];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t lds_base =
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds + wave * 8192;
+  uint32_t acc = 0;
+  for (int it = 0; it < kDmaBatches; ++it) {
+    // the wave's 8 KB window of the buffer moves by 8 KB per batch
+    const uint32_t win = ((blockIdx.x * WAVES + wave) * 8192u + it * 8192u) & (kDmaBufBytes - 1);
+    const uint32_t voff = win + lane * 16;
+    if (MODE == 0) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t m0 = lds_base + k * 1024;
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                     :
+                     : "v"(voff + k * 1024), "s"(src), "s"(m0)
+                     : "memory", "m0");
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+      u32x4 v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v[k]) : "v"(voff + k * 1024), "s"(src));
+      asm volatile("s_waitcnt vmcnt(0)" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]),
+                   "v"(v[5]), "v"(v[6]), "v"(v[7]));
+      if (MODE == 2) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          asm volatile("ds_write_b128 %0, %1" : : "v"(lds_base + k * 1024 + lane * 16), "v"(v[k]) : "memory");
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc ^= v[k][0];
+      }
+    }
+  }
+  __syncthreads();
+  out[blockIdx.x * 64 * WAVES + tid] = acc + lds[tid];
+}
+
 template <typename F>
 static float time_ms(F launch) {
   hipEvent_t e0, e1;
@@ -338,6 +396,40 @@ static int rates() {
   return 0;
 }
 
+static int dma() {
+  char* src;
+  uint32_t* out;
+  CHECK(hipMalloc(&src, kDmaBufBytes));
+  CHECK(hipMemset(src, 1, kDmaBufBytes));
+  CHECK(hipMalloc(&out, 256 * 512 * 4));
+  const char* names[3] = {"global_load_lds_dwordx4 (to LDS)", "global_load_dwordx4 (to VGPRs)",
+                          "global_load_dwordx4 + ds_write_b128"};
+  printf("Loads into a CU, 256 workgroups (one per CU), %d batches of 8 x 1 KB per wave, "
+         "1 MB L2-resident source:\n", kDmaBatches);
+  for (int waves : {4, 8})
+    for (int mode = 0; mode < 3; ++mode) {
+      float ms = time_ms([&] {
+        if (waves == 4) {
+          if (mode == 0) dma_kernel<0, 4><<<256, 256>>>(src, out);
+          else if (mode == 1) dma_kernel<1, 4><<<256, 256>>>(src, out);
+          else dma_kernel<2, 4><<<256, 256>>>(src, out);
+        } else {
+          if (mode == 0) dma_kernel<0, 8><<<256, 512>>>(src, out);
+          else if (mode == 1) dma_kernel<1, 8><<<256, 512>>>(src, out);
+          else dma_kernel<2, 8><<<256, 512>>>(src, out);
+        }
+      });
+      CHECK(hipGetLastError());
+      const double bytes_cu = (double)waves * kDmaBatches * 8 * 1024;
+      printf("  %d waves per CU, %-38s %.3f ms: %.0f B/ns per CU, %.1f TB/s total\n", waves,
+             names[mode], ms, bytes_cu / (ms * 1e6), 256 * bytes_cu / (ms * 1e9));
+    }
+  CHECK(hipDeviceSynchronize());
+  CHECK(hipFree(src));
+  CHECK(hipFree(out));
+  return 0;
+}
+
 static int lanes() {
   uint32_t* out;
   CHECK(hipMalloc(&out, 256));
@@ -357,6 +449,7 @@ static int lanes() {
 int main(int argc, char** argv) {
   if (argc == 2 && !strcmp(argv[1], "rates")) return rates();
   if (argc == 2 && !strcmp(argv[1], "lanes")) return lanes();
-  fprintf(stderr, "usage: %s rates|lanes\n", argv[0]);
+  if (argc == 2 && !strcmp(argv[1], "dma")) return dma();
+  fprintf(stderr, "usage: %s rates|lanes|dma\n", argv[0]);
   return 2;
 }
