@@ -738,10 +738,6 @@ __device__ __forceinline__ void sstep_zero_q(const lds_u8* slot, const HFrag& fa
   sub_pv(slot, fb, kb, w);
 }
 
-// One 32-key sub-block of a compensation step (the virtual keys of key
-// tiles key0 .. key0 + 31): p = exp2(s c - ref2) where the tile's weight
-// (its real row count if dropped, else 0) is positive, den += p * weight,
-// O^T += V^T P^T.
 // The 16 weights of this lane's keys key0 + 8 g + 4 hi + m of a sub-block.
 __device__ __forceinline__ void sub_weights(const uint8_t* wt, int key0, int hi, float (&ww)[16]) {
 #pragma unroll
@@ -752,22 +748,34 @@ __device__ __forceinline__ void sub_weights(const uint8_t* wt, int key0, int hi,
   }
 }
 
-__device__ __forceinline__ void sub_virtual(const lds_u8* slot, const HFrag& f, float c,
-                                            const uint8_t* wt, int key0, int hi, float ref2,
-                                            WaveState& w) {
-  const f32x16 s = sub_scores(slot, f, w, 32, hi);
-  float ww[16], ps[16], den = 0.f;
-  sub_weights(wt, key0, hi, ww);
+// A step of 64 virtual keys (the summaries of key tiles key0 .. key0 + 63)
+// of the compensation of a given output: both sub-blocks' score products as
+// interleaved chains (pair_scores, no key masked: virtual keys past n_k
+// carry weight 0); then per sub-block p = exp2(s c - ref2) where the tile's
+// weight (its real row count if dropped, else 0) is positive, den += p *
+// weight, and O^T += V^T P^T, sub-block a's terms before b's.
+__device__ __forceinline__ void vstep_fixed(const lds_u8* slot, const HFrag& fa, const HFrag& fb,
+                                            float c, const uint8_t* wt, int key0, int hi,
+                                            float ref2, WaveState& w) {
+  f32x16 sa, sb;
+  pair_scores(slot, fa, fb, w, 32, 32, hi, sa, sb);
+  auto probs = [&](const f32x16& s, int k0, u32x4 (&pk)[2]) {
+    float ww[16], ps[16], den = 0.f;
+    sub_weights(wt, k0, hi, ww);
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const float x = ww[e] > 0.f ? __builtin_amdgcn_exp2f(fmaf(s[e], c, -ref2)) : 0.f;
-    ps[e] = x;
-    den = fmaf(x, ww[e], den);
-  }
-  w.l_run += den;
-  u32x4 pk[2];
-  pack_probs(ps, pk);
-  sub_pv(slot, f, pk, w);
+    for (int e = 0; e < 16; ++e) {
+      const float x = ww[e] > 0.f ? __builtin_amdgcn_exp2f(fmaf(s[e], c, -ref2)) : 0.f;
+      ps[e] = x;
+      den = fmaf(x, ww[e], den);
+    }
+    w.l_run += den;
+    pack_probs(ps, pk);
+  };
+  u32x4 ka[2], kb[2];
+  probs(sa, key0, ka);
+  probs(sb, key0 + 32, kb);
+  sub_pv(slot, fa, ka, w);
+  sub_pv(slot, fb, kb, w);
 }
 
 // One step of 64 virtual keys inside the online softmax (compensated
@@ -855,6 +863,36 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   const int nk = (int)p.n_k_tiles;
 
   const int n_virt = VKEYS ? (nk + kHalf - 1) / kHalf : 0;
+  const SDma cdma = sdma_offsets(VKEYS ? p.cs : 0, VKEYS ? p.cs : 0, wave, lane);  // summaries
+  // Virtual step v: the summaries of key tiles 64 v .. 64 v + 63 (K and V
+  // halves of the slot); in the last step rows past n_k do not exist, so
+  // every lane reads a row below the step's count (the extra rows carry
+  // weight 0).
+  auto load_virtual = [&](int v, lds_u8* slot) {
+    const int64_t row0 = (int64_t)v * kHalf;
+    const int vch = min(nk - v * kHalf, kHalf);
+    const char* kb = reinterpret_cast<const char*>(p.kc + head * p.ch + row0 * p.cs);
+    const char* vb = reinterpret_cast<const char*>(p.vc + head * p.ch + row0 * p.cs);
+    if (vch == kHalf) {
+      // cdma's offsets of waves 2, 3 count from row 32
+      const int64_t sb = wave >= 2 ? 32 * p.cs * 2 : 0;
+#pragma unroll
+      for (int u4 = 0; u4 < 4; ++u4) {
+        dma16(kb + sb, cdma.k[u4], slot + (4 * wave + u4) * 1024);
+        dma16(vb + sb, cdma.v[u4], slot + kHalfBytes + (4 * wave + u4) * 1024);
+      }
+      return;
+    }
+    const int lr = lane >> 4, pc = lane & 15;
+#pragma unroll
+    for (int u4 = 0; u4 < 4; ++u4) {
+      const int seg = 4 * wave + u4, row = 4 * seg + lr, src = min(row, vch - 1);
+      const uint32_t ko = (uint32_t)((src * p.cs + ((pc ^ (row & 15)) << 3)) * 2);
+      const uint32_t vo = (uint32_t)((src * p.cs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
+      dma16(kb, ko, slot + seg * 1024);
+      dma16(vb, vo, slot + kHalfBytes + seg * 1024);
+    }
+  };
   if (VKEYS) {
     // weights of virtual keys 0 .. n_k - 1, padded with zeros to whole steps
     const uint8_t* keep_row = p.keep + (head * p.n_q_tiles + r) * p.n_k_tiles;
@@ -1028,36 +1066,13 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   const uint16_t* vbase = p.v + head * p.vh;
   const float c = p.scale_log2;
   const SDma dma = sdma_offsets(p.ks, p.vs, wave, lane);
-  const SDma cdma = sdma_offsets(VKEYS ? p.cs : 0, VKEYS ? p.cs : 0, wave, lane);  // summaries
   const HFrag fa = hfrag_offsets(0, lane), fb = hfrag_offsets(1, lane);
   auto load_step = [&](int u, lds_u8* slot) {
     int64_t row0, rowb;
     int vch, lb;
     decode(u, row0, vch, rowb, lb);
     if (VKEYS && u >= n_lsteps) {
-      // summaries; in the last step rows past n_k do not exist, so every
-      // lane reads a row below vch (the extra rows carry weight 0)
-      const char* kb = reinterpret_cast<const char*>(p.kc + head * p.ch + row0 * p.cs);
-      const char* vb = reinterpret_cast<const char*>(p.vc + head * p.ch + row0 * p.cs);
-      if (vch == kHalf) {
-        // cdma's offsets of waves 2, 3 count from row 32
-        const int64_t sb = wave >= 2 ? 32 * p.cs * 2 : 0;
-#pragma unroll
-        for (int u4 = 0; u4 < 4; ++u4) {
-          dma16(kb + sb, cdma.k[u4], slot + (4 * wave + u4) * 1024);
-          dma16(vb + sb, cdma.v[u4], slot + kHalfBytes + (4 * wave + u4) * 1024);
-        }
-        return;
-      }
-      const int lr = lane >> 4, pc = lane & 15;
-#pragma unroll
-      for (int u4 = 0; u4 < 4; ++u4) {
-        const int seg = 4 * wave + u4, row = 4 * seg + lr, src = min(row, vch - 1);
-        const uint32_t ko = (uint32_t)((src * p.cs + ((pc ^ (row & 15)) << 3)) * 2);
-        const uint32_t vo = (uint32_t)((src * p.cs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
-        dma16(kb, ko, slot + seg * 1024);
-        dma16(vb, vo, slot + kHalfBytes + seg * 1024);
-      }
+      load_virtual(u - n_lsteps, slot);
       return;
     }
     if (DENSE && vch < kHalf) {
@@ -1112,8 +1127,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     // keys past n_k carry weight 0 (the table is padded), so no mask
     const int key0 = (u - n_lsteps) * kHalf;
     if (MODE == kVirtualOnly) {
-      sub_virtual(cur, fa, c, vwt, key0, hi, ref2, w);
-      sub_virtual(cur, fb, c, vwt, key0 + 32, hi, ref2, w);
+      vstep_fixed(cur, fa, fb, c, vwt, key0, hi, ref2, w);
     } else {
       sstep_virtual(cur, fa, fb, c, vwt, key0, hi, w);
     }
@@ -1274,9 +1288,9 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   // den = 1 at the reference, hence out = (o_kept + num) / (1 + den)
   const bool row_real = !DENSE || qrow < p.used;
   const float inv = MODE == kVirtualOnly ? 1.f / (1.f + l) : (l > 0.f && row_real) ? 1.f / l : 0.f;
-  if (DENSE && qrow >= p.q_rows) return;  // rows past seq_len do not exist
-  uint16_t* orow = p.out + qrow * p.os + head * p.oh;
-  bool o_live = true;
+  const bool row_exists = !DENSE || qrow < p.q_rows;  // rows past seq_len do not exist
+  uint16_t* orow = p.out + (row_exists ? qrow : 0) * p.os + head * p.oh;
+  bool o_live = row_exists;
   if (MODE == kSparse && p.seq_o != nullptr) {
     const int64_t sh = p.seq_heads[head], dst = p.seq_o[qrow];
     o_live = p.slot_ok[qrow] != 0 && dst >= 0 && dst < p.out_rows && sh >= 0 &&
@@ -1284,13 +1298,20 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     orow = p.out + (o_live ? dst : 0) * p.os + (o_live ? sh : 0) * p.oh;
   }
   const uint16_t* krow = MODE == kVirtualOnly ? p.o_kept + qrow * p.oks + head * p.okh : nullptr;
+  // The output goes out as whole rows: each wave writes its 32 rows (bf16)
+  // into its 8 KB of the slot no step reads any more (the last step's is
+  // n_steps - 1's; every wave has passed the barrier after step n_steps - 2,
+  // which used this one), 16-byte chunk c of row r at c ^ (r % 16), then
+  // lane l stores chunk l % 16 of rows 4 i + l / 16: four rows per store
+  // instead of 16 bytes of each of 32 rows.
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  lds_u8* stage = (lds_u8*)ring[n_steps & 1] + wave * 8192;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int e = 4 * g;
       const int d = 32 * dt + 8 * g + 4 * hi;
-      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
       float kept4[4] = {0.f, 0.f, 0.f, 0.f};
       if (MODE == kVirtualOnly) {
         const u32x2 kv = *reinterpret_cast<const u32x2*>(krow + d);
@@ -1303,10 +1324,32 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         v4[m] = (MODE == kVirtualOnly ? kept4[m] + w.o[dt][e + m] : w.o[dt][e + m]) * inv;
-      uint32_t w0 = pack_bf16x2(v4[0], v4[1]), w1 = pack_bf16x2(v4[2], v4[3]);
-      if (o_live) *reinterpret_cast<u32x2*>(orow + d) = u32x2{w0, w1};
+      const uint32_t w0 = pack_bf16x2(v4[0], v4[1]), w1 = pack_bf16x2(v4[2], v4[3]);
+      *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(
+          stage + li * 256 + (((4 * dt + g) ^ (li & 15)) << 4) + 8 * hi) = u32x2{w0, w1};
     }
-  if ((MODE == kSparse || DENSE) && p.lse != nullptr && hi == 0)
+  asm volatile("" ::: "memory");
+  const uint64_t orow_bits = reinterpret_cast<uintptr_t>(orow);
+  const bool row16 = ((p.os | p.oh) & 7) == 0;  // every row start 16-byte aligned
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int rr = 4 * i + (lane >> 4), ch = lane & 15;
+    const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)orow_bits, rr);
+    const uint32_t up = (uint32_t)__shfl((int)(uint32_t)(orow_bits >> 32), rr);
+    const bool live = __shfl((int)o_live, rr) != 0;
+    const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+        stage + rr * 256 + ((ch ^ (rr & 15)) << 4));
+    uint16_t* dst = reinterpret_cast<uint16_t*>((uintptr_t)(((uint64_t)up << 32) | lo)) + 8 * ch;
+    if (live) {
+      if (row16) {
+        *reinterpret_cast<u32x4*>(dst) = v;
+      } else {  // rows 8-byte aligned only (strides that are multiples of 4 elements)
+        *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
+        *reinterpret_cast<u32x2*>(dst + 4) = u32x2{v[2], v[3]};
+      }
+    }
+  }
+  if ((MODE == kSparse || DENSE) && p.lse != nullptr && hi == 0 && row_exists)
     p.lse[head * p.lse_sh + qrow * p.lse_ss] =
         !row_real ? 0.f : l > 0.f ? (w.m_run + __log2f(l)) * kLn2 : -INFINITY;
 }
