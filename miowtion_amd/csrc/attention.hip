@@ -1112,10 +1112,28 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   // Step u: wait for its own loads (the only ones in flight), barrier (all
   // waves' loads of step u are in LDS and all are done reading the other
   // slot), issue step u + 1 into the other slot, compute step u.
+  // Compensation of a given output: o_kept's rows go to LDS as whole rows
+  // during the last step (into the slot the epilogue stages the output in,
+  // each wave its own 8 KB, with the output's layout) when every row start
+  // is 16-byte aligned; otherwise the epilogue reads them itself.
+  const bool kept_lds = MODE == kVirtualOnly &&
+                        ((reinterpret_cast<uintptr_t>(p.o_kept) & 15) | ((p.oks | p.okh) & 7)) == 0;
+  auto load_kept = [&](lds_u8* slot) {
+    const char* kb = reinterpret_cast<const char*>(p.o_kept + (r * kTile + 32 * wave) * p.oks +
+                                                   head * p.okh);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = 4 * i + (lane >> 4), ch = (lane & 15) ^ (rr & 15);
+      dma16(kb, (uint32_t)((rr * p.oks + 8 * ch) * 2), slot + wave * 8192 + i * 1024);
+    }
+  };
   auto begin_step = [&](int u, lds_u8* nxt) {
     VEDA_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
-    if (u + 1 < n_steps) load_step(u + 1, nxt);
+    if (u + 1 < n_steps)
+      load_step(u + 1, nxt);
+    else if (kept_lds)
+      load_kept(nxt);
   };
   auto list_step = [&](int u, const lds_u8* cur) {
     int64_t row0, rowb;
@@ -1306,6 +1324,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   // instead of 16 bytes of each of 32 rows.
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   lds_u8* stage = (lds_u8*)ring[n_steps & 1] + wave * 8192;
+  if (kept_lds) VEDA_WAIT_VM(0);  // this wave's o_kept rows are in its part of `stage`
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -1314,7 +1333,10 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       const int d = 32 * dt + 8 * g + 4 * hi;
       float kept4[4] = {0.f, 0.f, 0.f, 0.f};
       if (MODE == kVirtualOnly) {
-        const u32x2 kv = *reinterpret_cast<const u32x2*>(krow + d);
+        const u32x2 kv =
+            kept_lds ? *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(
+                           stage + li * 256 + (((4 * dt + g) ^ (li & 15)) << 4) + 8 * hi)
+                     : *reinterpret_cast<const u32x2*>(krow + d);
         kept4[0] = bf16_to_f32(kv[0] & 0xffffu);
         kept4[1] = bf16_to_f32(kv[0] >> 16);
         kept4[2] = bf16_to_f32(kv[1] & 0xffffu);
