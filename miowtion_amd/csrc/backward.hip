@@ -158,13 +158,6 @@ __device__ __forceinline__ void pack_b(const float (&x)[16], u32x4 (&pk)[2]) {
     for (int m = 0; m < 4; ++m) pk[kk][m] = pack_bf16x2(x[8 * kk + 2 * m], x[8 * kk + 2 * m + 1]);
 }
 
-// Stores 4 consecutive head-dims (accumulator values e0 .. e0 + 3) as bf16.
-__device__ __forceinline__ void store4(uint16_t* row, int d, const f32x16& a, int e0, float mul) {
-  const uint32_t w0 = pack_bf16x2(a[e0] * mul, a[e0 + 1] * mul);
-  const uint32_t w1 = pack_bf16x2(a[e0 + 2] * mul, a[e0 + 3] * mul);
-  *reinterpret_cast<u32x2*>(row + d) = u32x2{w0, w1};
-}
-
 // Wave 0 of a workgroup: the steps (target << 1 | half) of the full list,
 // then of the partial list, in list order; halves(t) = how many 64-row
 // halves of target t are steps (0 drops the entry). Returns the count.
@@ -398,11 +391,40 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
     run(u + 1, s1, s0);
   }
 
-  uint16_t* drow = p.dq + qrow * p.dqs + head * p.dqh;
+  // dQ leaves as whole rows: each wave writes its 32 bf16 rows into its
+  // 8 KB of the slot no step reads any more (the last step's is
+  // n_steps - 1's; every wave has passed the barrier after step
+  // n_steps - 2, which used this one), 16-byte chunk c of row r at
+  // c ^ (r % 16), then lane l stores chunk l % 16 of rows 4 i + l / 16:
+  // four rows per store instead of 16 bytes of each of 32 rows.
+  lds_u8* stage = (lds_u8*)ring[n_steps & 1] + wave * 8192;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) store4(drow, 32 * dt + 8 * g + 4 * hi, acc[dt], 4 * g, p.scale);
+    for (int g = 0; g < 4; ++g) {
+      const f32x16& a = acc[dt];
+      const int e0 = 4 * g;
+      const uint32_t w0 = pack_bf16x2(a[e0] * p.scale, a[e0 + 1] * p.scale);
+      const uint32_t w1 = pack_bf16x2(a[e0 + 2] * p.scale, a[e0 + 3] * p.scale);
+      *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(
+          stage + li * 256 + (((4 * dt + g) ^ (li & 15)) << 4) + 8 * hi) = u32x2{w0, w1};
+    }
+  asm volatile("" ::: "memory");
+  const bool row16 = ((reinterpret_cast<uintptr_t>(p.dq) & 15) | ((p.dqs | p.dqh) & 7)) == 0;
+  uint16_t* dbase = p.dq + (r * kTile + 32 * wave) * p.dqs + head * p.dqh;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int rr = 4 * i + (lane >> 4), ch = lane & 15;
+    const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+        stage + rr * 256 + ((ch ^ (rr & 15)) << 4));
+    uint16_t* dst = dbase + rr * p.dqs + 8 * ch;
+    if (row16) {
+      *reinterpret_cast<u32x4*>(dst) = v;
+    } else {  // rows 8-byte aligned only
+      *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
+      *reinterpret_cast<u32x2*>(dst + 4) = u32x2{v[2], v[3]};
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
