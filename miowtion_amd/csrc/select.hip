@@ -1,16 +1,18 @@
 // Block selection: equal-budget top-k per query tile, the block mask, and
 // the full / partial key-tile lists the attention kernel walks.
 //
-// Top-k: one wave per (head, query tile). The score row lives in LDS as
-// 64-bit keys (orderable fp32 score << 32 | ~column), lane-strided so every
-// LDS access is conflict-free; each lane caches the best key of its own
-// columns and k_hi rounds of a wave-wide max extract the winners in
-// descending order. The rounds are a latency chain, so occupancy is what
-// the kernel runs on: the LDS holds only the row's columns (dynamic size,
-// 20 KB per workgroup at 592 columns: 8 workgroups per CU instead of the 2
-// a 2048-column array allows). Folding the column into the key makes every key
-// distinct, so the order is total: higher score first, lower column first on
-// equal scores.
+// Top-k: one wave per (head, query tile). Scores become 64-bit keys
+// (orderable fp32 score << 32 | ~column); lane l holds the keys of columns
+// l, l + 64, .., sorts them in registers (a bitonic network over N = 16 or
+// 32 keys, zeros padding the list) and keeps them in LDS in that order,
+// lane-strided so every LDS access is conflict-free. k_hi rounds of a
+// wave-wide max over the lanes' current heads extract the winners in
+// descending order; the winning lane's next head is one LDS read. The
+// rounds are a latency chain, so occupancy is what the kernel runs on: the
+// LDS holds only the row's columns (dynamic size, 20 KB per workgroup at
+// 592 columns: 8 workgroups per CU instead of the 2 a 2048-column array
+// allows). Folding the column into the key makes every key distinct, so the
+// order is total: higher score first, lower column first on equal scores.
 //
 // Lists: one wave per (head, row), 64 columns per step, positions from a
 // ballot + popcount prefix (no sort, no atomics).
@@ -66,6 +68,27 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 constexpr int kMaxCols = 2048;  // columns of one block (FA4's 2048-block cap)
 constexpr int kSelWaves = 4;
 
+// Sorts N keys descending (bitonic network, indices fixed at compile time,
+// so the keys stay in registers).
+template <int N>
+__device__ __forceinline__ void sort_desc(uint64_t (&k)[N]) {
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1)
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const uint64_t a = k[i], b = k[j];
+          const bool sw = (i & size) == 0 ? a < b : a > b;
+          k[i] = sw ? b : a;
+          k[j] = sw ? a : b;
+        }
+      }
+}
+
+template <int N>  // keys per lane the registers hold (>= the row's columns / 64)
 __global__ void __launch_bounds__(256) select_topk_kernel(
     const float* __restrict__ scores, int64_t n_heads, int64_t n_rows, int64_t ssh,
     int64_t ssr, int64_t block_start, int n_cols, const uint8_t* __restrict__ kv_ok,
@@ -83,23 +106,25 @@ __global__ void __launch_bounds__(256) select_topk_kernel(
   const float* srow = scores + h * ssh + r * ssr + block_start;
   const int per_lane = (n_cols + 63) / 64;
   uint64_t* kv = keys + wave * per_lane * 64;
-  uint64_t best = 0;
-  int best_j = 0;
-  for (int j = 0; j < per_lane; ++j) {
+  uint64_t k[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
     const int c = j * 64 + lane;
     uint64_t key = 0;  // absent column: below every real key
-    if (c < n_cols) {
+    if (j < per_lane && c < n_cols) {
       float v = srow[c];
       if (!kv_ok[block_start + c]) v = -INFINITY;
       if (c == diag) v = INFINITY;
       key = ((uint64_t)orderable(v) << 32) | (uint32_t)(~(uint32_t)c);
     }
-    kv[j * 64 + lane] = key;
-    if (key > best) {
-      best = key;
-      best_j = j;
-    }
+    k[j] = key;
   }
+  sort_desc(k);
+#pragma unroll
+  for (int j = 0; j < N; ++j)
+    if (j < per_lane) kv[j * 64 + lane] = k[j];
+  uint64_t best = k[0];
+  int pos = 0;  // index of this lane's current head in its sorted list
   const bool has_extra = tile_id >= 0 && tile_id < n_extra && extra[tile_id] != 0;
   const int allowed = k_lo + (has_extra ? 1 : 0);
   int64_t* irow = index + h * osh + r * osr + col0;
@@ -111,16 +136,8 @@ __global__ void __launch_bounds__(256) select_topk_kernel(
     if ((int)(c & 63) == lane) {
       irow[t] = block_start + (int64_t)c;
       krow[t] = (t < allowed && vkey > kNegInfKey) ? 1 : 0;
-      kv[best_j * 64 + lane] = 0;
-      best = 0;
-      best_j = 0;
-      for (int j = 0; j < per_lane; ++j) {
-        const uint64_t key = kv[j * 64 + lane];
-        if (key > best) {
-          best = key;
-          best_j = j;
-        }
-      }
+      ++pos;
+      best = pos < per_lane ? kv[pos * 64 + lane] : 0;
     }
   }
 }
@@ -293,9 +310,16 @@ extern "C" int veda_select_topk(const float* scores, int64_t n_heads, int64_t n_
   if (items == 0) return VEDA_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const size_t lds = (size_t)kSelWaves * ((n_cols + 63) / 64) * 64 * sizeof(uint64_t);  // <= 64 KB
-  select_topk_kernel<<<(unsigned)((items + kSelWaves - 1) / kSelWaves), 256, lds, s>>>(
-      scores, n_heads, n_rows, s_stride_h, s_stride_r, block_start, (int)n_cols, kv_ok, rows,
-      (int)k_lo, (int)k_hi, extra, n_extra, index, keep, o_stride_h, o_stride_r, col0);
+  static_assert(32 * 64 >= kMaxCols, "select_topk_kernel<32> holds kMaxCols keys per wave");
+  const unsigned grid = (unsigned)((items + kSelWaves - 1) / kSelWaves);
+  if (n_cols <= 16 * 64)
+    select_topk_kernel<16><<<grid, 256, lds, s>>>(
+        scores, n_heads, n_rows, s_stride_h, s_stride_r, block_start, (int)n_cols, kv_ok, rows,
+        (int)k_lo, (int)k_hi, extra, n_extra, index, keep, o_stride_h, o_stride_r, col0);
+  else
+    select_topk_kernel<32><<<grid, 256, lds, s>>>(
+        scores, n_heads, n_rows, s_stride_h, s_stride_r, block_start, (int)n_cols, kv_ok, rows,
+        (int)k_lo, (int)k_hi, extra, n_extra, index, keep, o_stride_h, o_stride_r, col0);
   return check_launch("veda_select_topk");
 }
 
