@@ -142,3 +142,20 @@ def test_select_at_the_largest_column_count():
     scores[1, 5] = float('-inf')  # only the forced diagonal survives
     _run(scores, lay, olay, pm.column_blocks(lay, pm.Budget(ratio=0.1)),
          om.column_blocks(olay, om.Budget(ratio=0.1)))
+
+
+@pytest.mark.parametrize('thw,n_tiles', [((4, 64, 512), 1024), ((5, 40, 656), 1025),
+                                         ((11, 80, 160), 1100)])
+def test_select_around_the_key_list_sizes(thw, n_tiles):
+    """The top-k sorts each lane's keys in registers, 16 of them up to 1,024
+    columns and 32 above: the largest 16-key case, the smallest 32-key case
+    and a ragged one, with ties, bit-exact against the oracle."""
+    t, h, w = thw
+    spec = ([(0, thw)], t * h * w, t * h * w, '1x8x16')
+    lay, olay = _layouts(spec)
+    assert lay.n_tiles == n_tiles
+    g = torch.Generator().manual_seed(n_tiles)
+    scores = torch.rand(2, lay.n_video_tiles, lay.n_tiles, generator=g)
+    scores[1, ::5] = torch.randint(0, 4, (scores[1, ::5].shape), generator=g).float()  # ties
+    _run(scores, lay, olay, pm.column_blocks(lay, pm.Budget(ratio=0.1)),
+         om.column_blocks(olay, om.Budget(ratio=0.1)))
