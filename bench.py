@@ -8,11 +8,21 @@ diagonal -> 20,340 kept 128x128 blocks per head (90% sparsity).
 
 A step = one block-sparse attention forward over all 48 heads with the block
 lists prebuilt (the reference bench's "kernel" timing,
-miowtion/kernels/bench.py:87-126). Reported beside it: "+prep" (selection,
-block mask and lists rebuilt per call), the full Veda layer (gather + pool of
-q / k / v, predictor, selection, lists, sparse forward, scatter), the dense
-baselines at the same shape, the roofline of the sparse kernel and the CPU
-baseline (the oracle's masked-dense attention + predictor on host cores).
+miowtion/kernels/bench.py:87-126). As the reference bench does
+(:313-314, 337-343), the timed loop cycles through several seeded patterns
+(distinct uniform random score tensors, each giving 20,340 kept blocks per
+head), and before any rate is reported the output of every pattern is
+checked against fp32 masked attention of 3 query tiles x 2 heads computed
+with plain torch (:129-144, 315-333): the line carries the max error, a
+dense-match guard, and no TFLOP/s unless the error is within 2e-2.
+
+Reported beside it: "+prep" (selection, block mask and lists rebuilt per
+call), the full Veda layer (pooling of q, gather + pool of k, gather of v,
+predictor, selection, lists, sparse forward with the q permutation and the
+scatter fused in) on the same C2 patterns, the same layer with the lists of
+its random-weight predictor (labelled as such), the dense baselines at the
+same shape, the roofline of the sparse kernel and the CPU baseline (the
+oracle's masked-dense attention + predictor on host cores).
 
 Prints ONE JSON line. Effective TFLOP/s counts computed blocks only,
 4 * 128 * 128 * D per kept block (miowtion/kernels/bench.py:52-60).
@@ -21,6 +31,7 @@ Prints ONE JSON line. Effective TFLOP/s counts computed blocks only,
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import math
 import os
@@ -40,6 +51,8 @@ GRID = (37, 30, 52)
 HEADS = 48
 D = 128
 RATIO = 0.1
+PATTERNS = 4          # distinct seeded block patterns cycled in the timed loop
+CHECK_MAX_ERR = 2e-2  # fp32-reference bar a timed kernel must meet for its rate to count
 
 
 def _log(msg: str) -> None:
@@ -60,7 +73,9 @@ def _events_ms(fn, reps: int) -> list[float]:
     return out
 
 
-def build_case(seed: int = 0):
+def build_case(seed: int = 0, patterns: int = 1):
+    """The C2 layout, q / k / v and `patterns` seeded score tensors, each with
+    its block mask and lists (pattern 0 is the first draw after q, k, v)."""
     from miowtion_amd import kernels, mask as pm, tiling as pt
     used = GRID[0] * GRID[1] * GRID[2]
     seq_len = -(-used // 64) * 64
@@ -70,18 +85,53 @@ def build_case(seed: int = 0):
                for _ in range(3))
     for t in (q, k, v):
         t[used:] = 0
-    scores = torch.rand(HEADS, lay.n_tiles, lay.n_tiles, generator=g, device='cuda')
+    all_scores = [torch.rand(HEADS, lay.n_tiles, lay.n_tiles, generator=g, device='cuda')
+                  for _ in range(max(1, patterns))]
     qt, kt, vt = (kernels.gather_tiles(t, lay, None) for t in (q, k, v))
     blocks = pm.column_blocks(lay, pm.Budget(ratio=RATIO))
 
-    def prep():
-        sel = pm.select_video_blocks(scores, lay, blocks)
+    def prep(i: int = 0):
+        sel = pm.select_video_blocks(all_scores[i], lay, blocks)
         mask = pm.dense_block_mask(sel, lay)
         return mask, kernels.index_lists(mask, lay)
 
-    mask, lists = prep()
-    return dict(lay=lay, q=q, k=k, v=v, qt=qt, kt=kt, vt=vt, scores=scores, prep=prep,
-                mask=mask, lists=lists, used=used, seq_len=seq_len)
+    built = [prep(i) for i in range(len(all_scores))]
+    return dict(lay=lay, q=q, k=k, v=v, qt=qt, kt=kt, vt=vt, scores=all_scores[0],
+                all_scores=all_scores, prep=prep, mask=built[0][0], lists=built[0][1],
+                masks=[b[0] for b in built], all_lists=[b[1] for b in built],
+                used=used, seq_len=seq_len)
+
+
+def check_rows(c: dict, outs: list, tiles: list[int], heads: list[int]) -> dict:
+    """fp32 masked attention of query tiles `tiles` x `heads` with plain torch
+    (on the device, outside any timed region), against each pattern's
+    tile-ordered output in `outs`; also against dense attention (every key
+    tile kept), which a correct sparse output must be further from
+    (miowtion/kernels/bench.py:129-144, 315-333)."""
+    lay = c['lay']
+    key_ok = lay.slot_valid.bool()                               # [N] real key slots
+    scale = 1.0 / math.sqrt(D)
+    err = dense_err = 0.0
+    for mask, out in zip(c['masks'], outs):
+        for h in heads:
+            k = c['kt'][:, h].float()
+            v = c['vt'][:, h].float()
+            for i in tiles:
+                rows = slice(i * 128, (i + 1) * 128)
+                s = (c['qt'][rows, h].float() @ k.T) * scale                 # [128, N]
+                kept = mask[h, i].repeat_interleave(128) & key_ok
+                ref = torch.softmax(s.masked_fill(~kept[None], float('-inf')), -1) @ v
+                dense = torch.softmax(s.masked_fill(~key_ok[None], float('-inf')), -1) @ v
+                got = out[rows, h].float()
+                err = max(err, (got - ref).abs().max().item())
+                dense_err = max(dense_err, (got - dense).abs().max().item())
+    verdict = 'ok'
+    if not err <= CHECK_MAX_ERR:
+        verdict = f'WRONG: max_err {err:.3g} above {CHECK_MAX_ERR}'
+    elif dense_err < err:
+        verdict = 'WRONG: output matches dense attention'
+    return {'max_err': err, 'dense_err': dense_err, 'bar': CHECK_MAX_ERR, 'verdict': verdict,
+            'query_tiles': tiles, 'heads': heads, 'patterns': len(outs)}
 
 
 def cpu_baseline(budget_s: float = 20.0) -> dict:
@@ -350,11 +400,28 @@ def _backward(c: dict, kept: int, steps: int, warmup: int) -> int:
     return 0
 
 
+class _PatternScores:
+    """A predictor layer whose kernels run as usual and whose logits are then
+    overwritten with the next of the C2 pattern scores (so a full layer walks
+    the same block lists the kernel timing cycles through)."""
+
+    def __init__(self, base, scores: list, order):
+        self.base, self.scores, self.order = base, scores, order
+        self.second_order_rank = base.second_order_rank
+        self.count_gain = base.count_gain
+
+    def __call__(self, *args, **kw):
+        logits = self.base(*args, **kw)
+        return logits.copy_(self.scores[next(self.order) % len(self.scores)])
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=3)
+    ap.add_argument('--patterns', type=int, default=PATTERNS,
+                    help='distinct seeded C2 block patterns cycled in the timed loop')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-dense', action='store_true')
     ap.add_argument('--cpu-budget', type=float, default=20.0)
@@ -388,10 +455,12 @@ def main() -> int:
         print(json.dumps({'suite': suite(), 'gpu': torch.cuda.get_device_name(0)}), flush=True)
         return 0
     _log('bench: building C2 case')
-    c = build_case()
+    patterns = 1 if args.backward else args.patterns
+    c = build_case(patterns=patterns)
     lay = c['lay']
-    kept = int(c['mask'].sum())
-    assert kept == 20340 * HEADS, kept
+    kept_each = [int(m.sum()) for m in c['masks']]
+    assert all(k == 20340 * HEADS for k in kept_each), kept_each
+    kept = kept_each[0]
     if args.backward:
         return _backward(c, kept, args.steps, args.warmup)
     flop = 4.0 * 128 * 128 * D * kept
@@ -399,15 +468,22 @@ def main() -> int:
     # rows of partial key tiles are neither loaded nor multiplied), for all
     # 128 query rows in the P.V products and for the 32-row groups that hold
     # a real row in the Q.K^T products (a group of padding rows, all zero,
-    # skips them).
+    # skips them); averaged over the patterns.
     vc = lay.valid_count.float()
-    keys_per_row = (c['mask'].float() * vc[None, None, :]).sum(-1)          # [H, R]
-    live_groups = torch.ceil(vc[:keys_per_row.shape[1]] / 32.0)             # per query tile
-    exec_flop = float((keys_per_row * (2.0 * 128 * D + 2.0 * 32 * D * live_groups[None, :])).sum())
+    live_groups = torch.ceil(vc / 32.0)                                     # per query tile
+    exec_flop = 0.0
+    for m in c['masks']:
+        keys_per_row = (m.float() * vc[None, None, :]).sum(-1)              # [H, R]
+        exec_flop += float((keys_per_row * (2.0 * 128 * D
+                                            + 2.0 * 32 * D * live_groups[None, :])).sum())
+    exec_flop /= len(c['masks'])
     dense_flop = 4.0 * c['used'] * c['used'] * HEADS * D
+    order = itertools.count()
 
     def step():
-        return kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'], c['lists'], lay)
+        i = next(order) % patterns
+        return kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'], c['all_lists'][i],
+                                                    lay)
 
     _log(f'bench: warmup {args.warmup}')
     for _ in range(args.warmup):
@@ -423,22 +499,39 @@ def main() -> int:
     k_ms = kernel_ms[len(kernel_ms) // 2]
     k_avg = sum(kernel_ms) / len(kernel_ms)
     achieved = flop / (k_avg * 1e-3) / 1e12
+    # the check runs after the timed region on each pattern's own output
+    _log('bench: checking every pattern against fp32 rows')
+    n = lay.n_tiles
+    check = check_rows(c, [kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'], li, lay)
+                           for li in c['all_lists']], [0, n // 3, n - 1], [0, HEADS - 1])
+    valid = check['verdict'] == 'ok'
+    if not valid:
+        _log(f"bench: {check['verdict']}: no rate is reported")
     if args.only_kernel:
-        print(json.dumps({'metric': METRIC, 'value': round(flop / (k_ms * 1e-3) / 1e12, 2),
+        print(json.dumps({'metric': METRIC,
+                          'value': round(flop / (k_ms * 1e-3) / 1e12, 2) if valid else None,
                           'ms_per_step': round(k_ms, 4), 'avg_launch_ms': round(k_avg, 4),
-                          'only_kernel': True}), flush=True)
-        return 0
+                          'check': check, 'only_kernel': True}), flush=True)
+        return 0 if valid else 1
 
     _log('bench: +prep and full layer')
-    prep_ms = sorted(_events_ms(lambda: c['prep'](), 5))[2]
+    prep_ms = sorted(_events_ms(lambda: c['prep'](next(order) % patterns), 5))[2]
     from miowtion_amd import attention as pa, plan as pplan, predictor as pp, tiling as pt
     layout = pa.PackedLayout((pa.VideoSpan(0, GRID),), c['used'], c['seq_len'])
     clip = pa.ClipTiling(layout, pa.VedaConfig(target_budget=pm.Budget(ratio=RATIO)), 'cuda')
     plan = pplan.TilePlan.uniform('16x9_t37_c2', GRID, pt.TileShape(1, 8, 16), 1, HEADS)
-    pred = pp.TileScorePredictor([pp.LayerPredictor.random(
-        HEADS, D, std=0.02, generator=torch.Generator().manual_seed(1), device='cuda', fp8=True)])
-    student = pa.SparseStudent(clip, plan, pred)
-    layer_ms = sorted(_events_ms(lambda: student(c['q'], c['k'], c['v'], 0), 5))[2]
+    base = pp.LayerPredictor.random(HEADS, D, std=0.02, generator=torch.Generator().manual_seed(1),
+                                    device='cuda', fp8=True)
+    # The whole layer on the timed C2 patterns: the predictor's kernels run
+    # as in the real layer, then its logits are overwritten with the next C2
+    # pattern's scores (one 67 MB device copy more than the real layer), so
+    # the sparse forward walks the same lists as the kernel timing above.
+    student = pa.SparseStudent(clip, plan, pp.TileScorePredictor(
+        [_PatternScores(base, c['all_scores'], order)]))
+    layer_ms = sorted(_events_ms(lambda: student(c['q'], c['k'], c['v'], 0), 7))[3]
+    # the same layer on its random-weight predictor's own lists
+    student_p = pa.SparseStudent(clip, plan, pp.TileScorePredictor([base]))
+    layer_pred_ms = sorted(_events_ms(lambda: student_p(c['q'], c['k'], c['v'], 0), 7))[3]
 
     dense = {}
     if not args.no_dense:
@@ -463,7 +556,7 @@ def main() -> int:
 
     line = {
         'metric': METRIC,
-        'value': round(flop / (k_ms * 1e-3) / 1e12, 2),
+        'value': round(flop / (k_ms * 1e-3) / 1e12, 2) if valid else None,
         'unit': 'TFLOP/s (effective, computed blocks)',
         'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
         'ms_per_step': round(k_ms, 4),
@@ -476,12 +569,23 @@ def main() -> int:
                    'kept_blocks': kept, 'flop_per_launch': flop,
                    'executed_flop_per_launch': exec_flop,
                    'dense_equivalent_flop': dense_flop},
+        'n_patterns': patterns,
+        'check': check,
         'ms_per_layer': {'kernel': round(k_ms, 4), 'plus_prep': round(k_ms + prep_ms, 4),
-                         'prep': round(prep_ms, 4), 'full_veda_layer': round(layer_ms, 4)},
+                         'prep': round(prep_ms, 4), 'full_veda_layer': round(layer_ms, 4),
+                         'full_veda_layer_predictor_lists': round(layer_pred_ms, 4),
+                         'note': 'full_veda_layer: pooling, gathers, predictor, selection, '
+                                 'lists, sparse forward with the q permutation and scatter '
+                                 'fused in, on the timed C2 patterns; '
+                                 'full_veda_layer_predictor_lists: the same layer on the lists '
+                                 'of its random-weight predictor, which are far more alike '
+                                 'across query tiles than C2 uniform random scores'},
         'dense_equivalent_tflops': round(dense_flop / (k_ms * 1e-3) / 1e12, 2),
         'dense': dense,
-        'roofline': {'bound': 'mfma', 'achieved': round(achieved, 2), 'peak': PEAK_BF16_TFLOPS,
-                     'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_BF16_TFLOPS, 4),
+        'roofline': {'bound': 'mfma', 'achieved': round(achieved, 2) if valid else None,
+                     'peak': PEAK_BF16_TFLOPS,
+                     'unit': 'TFLOP/s',
+                     'frac': round(achieved / PEAK_BF16_TFLOPS, 4) if valid else None,
                      'traffic': _traffic(), 'kernel': 'sfwd_kernel (veda_block_sparse_fwd)',
                      'avg_launch_ms': round(k_avg, 4),
                      'achieved_on_executed_flop': round(exec_flop / (k_avg * 1e-3) / 1e12, 2),
@@ -490,7 +594,7 @@ def main() -> int:
         'cpu_baseline': cpu,
     }
     print(json.dumps(line), flush=True)
-    return 0
+    return 0 if valid else 1
 
 
 if __name__ == '__main__':

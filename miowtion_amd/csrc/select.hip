@@ -24,13 +24,19 @@
 namespace veda {
 namespace {
 
+// Order key of a score: unsigned order of keys = numeric order of scores,
+// with every NaN (either sign) one key above +inf, as torch.sort / topk rank
+// NaN above every number (so NaNs tie among themselves and fall back to
+// column order).
+constexpr uint32_t kNaNKey = 0xffffffffu;
+constexpr uint32_t kNegInfKey = 0x007fffffu;  // orderable(-inf)
+
 __device__ __forceinline__ uint32_t orderable(float v) {
+  if (v != v) return kNaNKey;
   if (v == 0.f) v = 0.f;  // -0 ties with +0, as in a float comparison
   uint32_t u = __float_as_uint(v);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
-
-constexpr uint32_t kNegInfKey = 0x007fffffu;  // orderable(-inf)
 
 template <int CTRL>
 __device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
@@ -135,7 +141,9 @@ __global__ void __launch_bounds__(256) select_topk_kernel(
     const uint32_t vkey = (uint32_t)(top >> 32);
     if ((int)(c & 63) == lane) {
       irow[t] = block_start + (int64_t)c;
-      krow[t] = (t < allowed && vkey > kNegInfKey) ? 1 : 0;
+      // kept: within the row's budget and `val > -inf` (False for NaN,
+      // mask.py:251-284)
+      krow[t] = (t < allowed && vkey > kNegInfKey && vkey != kNaNKey) ? 1 : 0;
       ++pos;
       best = pos < per_lane ? kv[pos * 64 + lane] : 0;
     }

@@ -140,9 +140,9 @@ __global__ void __launch_bounds__(64 * WAVES) gather_kernel(
       for (int e = 0; e < 8; ++e) {
         const float f = elem(r, e);
         s_sum[e] += f;
-        if (real) {
-          s_max[e] = fmaxf(s_max[e], f);
-          s_min[e] = fminf(s_min[e], f);
+        if (real) {  // NaN-propagating, as torch's amax / amin
+          s_max[e] = __builtin_elementwise_maximum(s_max[e], f);
+          s_min[e] = __builtin_elementwise_minimum(s_min[e], f);
         }
         if (SECOND) s_sq[e] += f * f;
       }
@@ -174,8 +174,8 @@ __global__ void __launch_bounds__(64 * WAVES) gather_kernel(
 #pragma unroll
       for (int w = 1; w < WAVES; ++w) {
         a += red[0][w][lane][e];
-        b = fmaxf(b, red[1][w][lane][e]);
-        c = fminf(c, red[2][w][lane][e]);
+        b = __builtin_elementwise_maximum(b, red[1][w][lane][e]);
+        c = __builtin_elementwise_minimum(c, red[2][w][lane][e]);
         if (SECOND) d += red[kStats - 1][w][lane][e];
       }
       mean[e] = a / denom;
@@ -345,11 +345,16 @@ __global__ void __launch_bounds__(64 * kWaves, kPoolOccupancy) pool_gather_kerne
       mx.w[w] = __builtin_bit_cast(uint32_t, order_key(k_max[w]));  // the key map is its own inverse
       mn.w[w] = __builtin_bit_cast(uint32_t, order_key(k_min[w]));
     }
+    // A NaN of either sign among the real rows makes both max and min NaN,
+    // as torch's amax / amin propagate it: a +NaN key orders above +inf's
+    // and a -NaN key below -inf's, so one of the two accumulators holds it.
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
+      const float a = elem(mx, e), b = elem(mn, e);
+      const bool nan = a != a || b != b;
       s_sum[e] = empty ? 0.f : s_sum[e] / denom;
-      s_max[e] = empty ? 0.f : elem(mx, e);
-      s_min[e] = empty ? 0.f : elem(mn, e);
+      s_max[e] = empty ? 0.f : nan ? __builtin_nanf("") : a;
+      s_min[e] = empty ? 0.f : nan ? __builtin_nanf("") : b;
     }
   }
 #pragma unroll

@@ -113,12 +113,10 @@ def pool_tiles(x: torch.Tensor, layout: tiling.TileLayout, second: str | None = 
 
 
 def _identity(layout: tiling.TileLayout) -> torch.Tensor:
-    """arange(num_slots) on the layout's device, kept on the layout."""
-    hit = layout.derived.get('identity')
-    if hit is None:
-        hit = torch.arange(layout.num_slots, device=layout.valid_count.device)
-        layout.derived['identity'] = hit
-    return hit
+    """arange(num_slots) on the layout's device, cached for the layout."""
+    return tiling.layout_cached(
+        layout, 'identity',
+        lambda: torch.arange(layout.n_tiles * tiling.TILE_SIZE, device=layout.valid_count.device))
 
 
 def scatter_tiles_(out: torch.Tensor, tiled: torch.Tensor, layout: tiling.TileLayout,

@@ -124,6 +124,11 @@ class TilePlan:
         try:
             with os.fdopen(fd, 'w') as f:
                 json.dump(self.to_json(), f, indent=1)
+            # mkstemp creates the file 0600; give it the mode open() would
+            # (0666 less the umask), as the reference's writer does
+            umask = os.umask(0)
+            os.umask(umask)
+            os.chmod(tmp, 0o666 & ~umask)
             os.replace(tmp, path)
         except BaseException:
             if os.path.exists(tmp):

@@ -146,10 +146,8 @@ class TileScorePredictor:
 
 
 def log_count(layout: tiling.TileLayout) -> torch.Tensor:
-    """log(max(valid_count, 1)) per key tile, kept on the layout (so it
+    """log(max(valid_count, 1)) per key tile, cached for the layout (so it
     lives exactly as long as the layout does)."""
-    hit = layout.derived.get('log_count')
-    if hit is None:
-        hit = torch.log(layout.valid_count.clamp(min=1).to(torch.float32))
-        layout.derived['log_count'] = hit
-    return hit
+    return tiling.layout_cached(
+        layout, 'log_count',
+        lambda: torch.log(layout.valid_count.clamp(min=1).to(torch.float32)))

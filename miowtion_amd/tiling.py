@@ -18,6 +18,7 @@ from __future__ import annotations
 import dataclasses
 import itertools
 import math
+import weakref
 from collections.abc import Callable, Sequence
 
 import numpy as np
@@ -145,9 +146,6 @@ class TileLayout:
     kv_ok: torch.Tensor
     full_tile: torch.Tensor
     slot_valid: torch.Tensor
-    # Small tensors derived from the layout (per-tile log counts, an
-    # identity index), built on first use and dropped with the layout.
-    derived: dict = dataclasses.field(default_factory=dict, repr=False, compare=False)
 
     @property
     def n_tiles(self) -> int:
@@ -156,6 +154,27 @@ class TileLayout:
     @property
     def num_slots(self) -> int:
         return self.n_tiles * TILE_SIZE
+
+
+# Small tensors derived from a layout (per-tile log counts, an identity
+# index), keyed by the layout object's identity and dropped when it is
+# collected. The layout itself carries only the reference's fields, so a
+# layout built by the reference's own builder works here unchanged (its
+# dataclass is unhashable, hence the identity key).
+_DERIVED: dict[int, dict[str, torch.Tensor]] = {}
+
+
+def layout_cached(layout, key: str, build: Callable[[], torch.Tensor]) -> torch.Tensor:
+    """The tensor `build()` for this layout object, built on first use and
+    kept until the layout is garbage collected."""
+    entry = _DERIVED.get(id(layout))
+    if entry is None:
+        entry = _DERIVED[id(layout)] = {}
+        weakref.finalize(layout, _DERIVED.pop, id(layout), None)
+    hit = entry.get(key)
+    if hit is None:
+        hit = entry[key] = build()
+    return hit
 
 
 def build_tile_layout(spans: Sequence[TiledSpan], used: int, seq_len: int,

@@ -50,6 +50,3 @@ def qkv(seq_len, heads=4, dim=128, seed=0, n=3):
     return [torch.randn(seq_len, heads, dim, generator=g).to(torch.bfloat16) for _ in range(n)]
 
 
-def oracle_copy(lay):
-    """The oracle layout with the same permutation as a product layout."""
-    return lay

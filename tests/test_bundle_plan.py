@@ -11,6 +11,8 @@ library routine the reference calls) and by the per-head amax / 448 rule.
 """
 
 import json
+import os
+import stat
 import pathlib
 
 import pytest
@@ -251,6 +253,10 @@ def test_plan_json_round_trips_the_released_file_unchanged(tmp_path):
     plan.save(str(out))
     assert json.loads(out.read_text()) == raw
     assert [p.name for p in tmp_path.iterdir()] == ['p.json']   # no temporary left behind
+    # the mode open(path, 'w') gives, as the reference's writer (0666 less the umask)
+    umask = os.umask(0)
+    os.umask(umask)
+    assert stat.S_IMODE(out.stat().st_mode) == 0o666 & ~umask
     with pytest.raises(ValueError, match='at most 2'):
         pplan.TilePlan('g', (1, 8, 16), [pt.TileShape.parse(s) for s in ('1x8x16', '2x8x8',
                                                                              '4x4x8')],

@@ -56,6 +56,40 @@ def test_sparse_matches_oracle_with_partial_tiles():
     _close(lse.T, ref_lse.T, real)
 
 
+def test_non_finite_values_stay_in_the_query_tiles_that_keep_them():
+    """An Inf in V reaches only the query tiles that keep its key tile, as in
+    the reference (whose rows there become Inf, or NaN where p underflows to
+    0, through P.V). The kernel does not reload a step's key rows past a
+    sub-block's valid count, so those slot rows hold V rows of tiles that
+    the same query tile kept in earlier steps; multiplied by p = 0 they can
+    only turn an element the reference makes Inf into NaN, never make a
+    finite element non-finite. Checked with Inf in ragged tiles (16 and 32
+    valid keys, whose halves share steps) and in a full tile: the finite
+    mask equals the oracle's element for element, and the finite elements
+    meet the usual bar."""
+    spec = helpers.small_layout(grid=(5, 12, 20), shape='2x8x8')
+    lay, olay, qt, kt, vt, mask = _case(spec, heads=2, ratio=0.5, seed=7)
+    vc = olay.valid_count
+    ragged = [int(t) for t in torch.nonzero((vc > 0) & (vc <= 32)).flatten()[:2]]
+    full = int(torch.nonzero(vc == 128).flatten()[0])
+    vinf = vt.clone()
+    expect = torch.ones(qt.shape, dtype=torch.bool)           # finite elements
+    for t, d in zip(ragged + [full], (3, 70, 127)):
+        vinf[t * 128 + int(vc[t]) - 1, 0, d] = float('inf')
+        # rows of every query tile that keeps tile t, head 0, column d
+        expect.view(-1, 128, 2, 128)[mask[0, :, t], :, 0, d] = False
+    out = kernels.block_sparse_attention(qt.cuda(), kt.cuda(), vinf.cuda(), mask.cuda(), lay).cpu()
+    # the oracle's masked-dense product multiplies every masked key too (0 x
+    # Inf would poison every row), so its values come from the finite V: a
+    # value row changes nothing but its own column of the rows that keep it
+    ref = oa.block_sparse_attention(qt, kt, vt, mask, olay.valid_count)
+    real = olay.slot_valid.bool()
+    got, fin, want = out.float()[real], expect[real], ref.float()[real]
+    assert (~fin).any() and fin.any()
+    assert torch.equal(torch.isfinite(got), fin)
+    assert (got[fin] - want[fin]).abs().max().item() <= MAX_ABS
+
+
 def test_keep_all_sparse_equals_dense_kernel_and_oracle():
     # reference tests/gpu/test_kernels_gpu.py:115-138
     spec = helpers.small_layout()
@@ -145,10 +179,12 @@ def test_dense_matches_oracle(seq_len, used):
     assert (out[used:] == 0).all() and (lse[used:] == 0).all()
 
 
-def test_sampled_query_tiles_at_config2_size():
-    """C2 geometry (592 tiles, 48 heads) at 90% sparsity: sampled query tiles
-    of the full-size kernel call against the oracle (size-independent check:
-    every row's output is a convex combination of its kept values)."""
+def test_whole_heads_at_config2_size():
+    """C2 geometry (592 tiles, 48 heads) at 90% sparsity: every query tile of
+    two heads (the first and the last) of the full-size kernel call against
+    the oracle. The step walk (full-list halves, split halves, ragged halves
+    paired two to a step) differs from tile to tile, so whole heads cover
+    every form it takes on this workload."""
     spec = helpers.CONFIGS['C2']
     lay = helpers.product_layout(*spec, device='cuda')
     olay = helpers.oracle_layout(*spec)
@@ -162,17 +198,14 @@ def test_sampled_query_tiles_at_config2_size():
     mask = pm.dense_block_mask(sel, lay)
     out, lse = kernels.block_sparse_attention(qt, kt, vt, mask, lay, return_lse=True)
     assert torch.isfinite(out.float()).all()
-    rows = torch.tensor([0, 17, 333, 591])
     heads = [0, 47]
-    sub_q = qt.view(-1, 128, H, 128)[rows.cuda()].reshape(-1, H, 128)[:, heads].cpu()
-    sub_m = mask[heads][:, rows.cuda()].cpu()
-    ref, ref_lse = oa.block_sparse_attention(sub_q, kt[:, heads].cpu(), vt[:, heads].cpu(), sub_m,
+    print(f'C2 whole heads {heads}: {lay.n_tiles} query tiles each against the oracle', flush=True)
+    ref, ref_lse = oa.block_sparse_attention(qt[:, heads].cpu(), kt[:, heads].cpu(),
+                                             vt[:, heads].cpu(), mask[heads].cpu(),
                                              olay.valid_count, return_lse=True)
-    got = out.view(-1, 128, H, 128)[rows.cuda()].reshape(-1, H, 128)[:, heads]
-    got_lse = lse.view(H, -1, 128)[heads][:, rows.cuda()].reshape(len(heads), -1)
-    real = olay.slot_valid.view(-1, 128)[rows].reshape(-1).bool()
-    _close(got, ref, real)
-    _close(got_lse.T, ref_lse.T, real)
+    real = olay.slot_valid.bool()
+    _close(out[:, heads], ref, real)
+    _close(lse[heads].T, ref_lse.T, real)
 
 
 def test_front_tiles_change_the_order_only():

@@ -112,20 +112,23 @@ def test_config3_layer_at_full_size():
             assert torch.equal(a.cpu(), b)
         # 40,680 kept blocks per head at keep 0.2 for both shapes (equal cost)
         assert int((mask & olay.kv_ok[None, None, :]).sum()) == 40680 * heads.numel()
-        # sampled query tiles: the first, a padded (partial) one, the last
+        # every query tile of the group's first head; the first, a padded
+        # (partial) and the last tile of its last head
         partial = int(olay.partial_tiles[len(olay.partial_tiles) // 2])
-        tiles = torch.tensor([0, partial, olay.n_tiles - 1])
-        hs = heads[[0, -1]]
-        rows = _tile_rows(tiles)
-        qt = ot.gather_tiles(q[:, hs.cuda()].cpu(), olay, None)[rows]
-        kt = ot.gather_tiles(k[:, hs.cuda()].cpu(), olay, None)
-        vt = ot.gather_tiles(v[:, hs.cuda()].cpu(), olay, None)
-        hpos = [heads.tolist().index(h) for h in hs.tolist()]
-        ref = oa.block_sparse_attention(qt, kt, vt, mask[hpos][:, tiles], olay.valid_count)
-        real = olay.slot_valid[rows].bool()
-        seq_rows = olay.perm[rows][real]
-        got = out[seq_rows.cuda()][:, hs.cuda()].cpu()
-        _close(got, ref[real])
+        for hs, tiles in ((heads[[0]], torch.arange(olay.n_tiles)),
+                          (heads[[-1]], torch.tensor([0, partial, olay.n_tiles - 1]))):
+            rows = _tile_rows(tiles)
+            print(f'C3 group {shape}: head {int(hs[0])}, {tiles.numel()} query tiles against the '
+                  'oracle', flush=True)
+            qt = ot.gather_tiles(q[:, hs.cuda()].cpu(), olay, None)[rows]
+            kt = ot.gather_tiles(k[:, hs.cuda()].cpu(), olay, None)
+            vt = ot.gather_tiles(v[:, hs.cuda()].cpu(), olay, None)
+            hpos = [heads.tolist().index(h) for h in hs.tolist()]
+            ref = oa.block_sparse_attention(qt, kt, vt, mask[hpos][:, tiles], olay.valid_count)
+            real = olay.slot_valid[rows].bool()
+            seq_rows = olay.perm[rows][real]
+            got = out[seq_rows.cuda()][:, hs.cuda()].cpu()
+            _close(got, ref[real])
 
 
 def test_config5_oracle_chain_at_full_size():

@@ -227,12 +227,31 @@ def test_config4_predictor_and_selection_at_config2_geometry(contiguous):
     sel = pm.select_video_blocks(got[:, :nv].cuda(), lay, pm.column_blocks(lay, pm.Budget(ratio=0.1)))
     idx, keep = om.select_video_blocks(got[:, :nv], olay, om.column_blocks(olay, om.Budget(ratio=0.1)))
     assert torch.equal(sel.index.cpu(), idx) and torch.equal(sel.keep.cpu(), keep)
+    blocks = om.column_blocks(olay, om.Budget(ratio=0.1))
+
+    def mask_of(logits):
+        return om.dense_block_mask(*om.select_video_blocks(logits[:, :nv], olay, blocks), olay)
+
     mask_got = om.dense_block_mask(idx, keep, olay)
-    idx2, keep2 = om.select_video_blocks(want[:, :nv], olay, om.column_blocks(olay, om.Budget(ratio=0.1)))
-    mask_ref = om.dense_block_mask(idx2, keep2, olay)
-    flips = int((mask_got != mask_ref).sum()) / max(int(mask_ref.sum()), 1)
-    print(f'config 4 ({lay.n_tiles} tiles): kept-block flip rate vs oracle logits {flips:.2e}')
-    assert flips < 1e-2
+    mask_ref = mask_of(want)
+    # the two summation-order terms apart: the oracle's GEMMs on the kernel's
+    # pooled features isolate the pooling (mean) order from the GEMM order
+    mixed = op.logits(fq.cpu(), fk.cpu(), _oracle_weight(pred.proj_q), _oracle_weight(pred.proj_k),
+                      heads)
+    mask_mix = mask_of(mixed)
+    kept = int(mask_ref.sum())
+    flips = int((mask_got != mask_ref).sum())
+    pool_flips = int((mask_mix != mask_ref).sum())
+    gemm_flips = int((mask_got != mask_mix).sum())
+    gap = (got - want).abs().max().item()
+    print(f'config 4 ({lay.n_tiles} tiles, 2 heads, {kept} kept blocks): flipped blocks vs the '
+          f'oracle logits {flips} (rate {flips / kept:.2e}); pooling order alone {pool_flips}, '
+          f'GEMM order alone {gemm_flips}; max |logit difference| {gap:.2e}', flush=True)
+    # Measured on MI355X: 0 flipped blocks for both tilers (the logits differ
+    # by <= 1e-4 of their scale, far below the gaps at the k-th rank). A
+    # single near-tie swaps one kept block for another (2 flipped entries);
+    # the bound allows one such swap per head and nothing more.
+    assert flips <= 2 * 2, flips
 
 
 def test_e4m3_decode_matches_torch_for_every_code():

@@ -64,6 +64,42 @@ def test_select_ties_follow_the_stable_order():
     _run(scores, lay, olay, pb, ob)
 
 
+def test_select_nan_scores_rank_first_and_are_never_kept():
+    """torch.topk / torch.sort rank every NaN, of either sign, above +inf, and
+    the reference keeps an entry only where `val > -inf`, which is False for
+    NaN (mask.py:251-284): NaN columns take the first positions of the index
+    and are never kept. The oracle follows torch.sort (pinned against
+    torch.topk in test_oracle_mask.py); the kernel must match it bit for
+    bit. Rows with more NaNs than k_hi, NaN on the own-tile diagonal (the
+    diagonal is forced to +inf) and NaN on empty tiles (forced to -inf) are
+    all covered."""
+    lay, olay = _layouts(_spec_with_cond())
+    nv = lay.n_video_tiles
+    g = torch.Generator().manual_seed(5)
+    scores = torch.randn(3, nv, lay.n_tiles, generator=g)
+    pick = torch.rand(scores.shape, generator=g)
+    nan = torch.tensor(float('nan'))
+    scores = torch.where(pick < 0.05, nan, scores)
+    scores = torch.where((pick >= 0.05) & (pick < 0.08), -nan, scores)
+    scores = torch.where((pick >= 0.08) & (pick < 0.09), torch.tensor(float('inf')), scores)
+    scores = torch.where((pick >= 0.09) & (pick < 0.10), torch.tensor(float('-inf')), scores)
+    assert torch.signbit(scores[(pick >= 0.05) & (pick < 0.08)]).all()
+    scores[1, 3] = nan                       # a row of NaN only
+    scores[2, 4] = -nan
+    rows = torch.arange(nv)
+    scores[0, rows, rows] = nan              # NaN on every diagonal
+    pb = pm.column_blocks(lay, pm.Budget(ratio=0.25), pm.Budget(tiles=2.5))
+    ob = om.column_blocks(olay, om.Budget(ratio=0.25), om.Budget(tiles=2.5))
+    sel, ri, rk = _run(scores, lay, olay, pb, ob)
+    flat_s = scores.gather(-1, ri)
+    # the own tile is forced to +inf, so its NaN score does not count; NaN
+    # columns rank ahead of it and can push it past the row's budget
+    own = ri == torch.arange(nv)[None, :, None]
+    assert not rk[torch.isnan(flat_s) & ~own].any()
+    mask = pm.dense_block_mask(sel, lay).cpu()
+    assert torch.equal(mask, om.dense_block_mask(ri, rk, olay))
+
+
 def test_select_keep_all_and_budget_above_columns():
     lay, olay = _layouts(helpers.small_layout())
     scores = torch.rand(2, lay.n_video_tiles, lay.n_tiles, generator=torch.Generator().manual_seed(3))

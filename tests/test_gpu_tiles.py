@@ -55,6 +55,39 @@ def test_second_moments_match_oracle():
     assert torch.equal(kernels.pool_tiles(tiles, lay, 'central'), var)
 
 
+@pytest.mark.parametrize('second', [False, True])
+def test_pooling_propagates_nan_like_torch(second):
+    """torch's amax / amin return NaN when a reduced row holds NaN, of either
+    sign (the reference pools with them, predictor.py:82-130). Both pooling
+    forms (the packed int16 order keys of first-order pooling, and the
+    4-wave form with second moments) must do the same: tiles with +NaN only,
+    -NaN only, both, and +inf beside -inf (max / min stay finite-signed,
+    the mean is NaN)."""
+    lay, olay = _pair(helpers.small_layout())
+    x, = helpers.qkv(lay.seq_len, 2, 128, seed=6, n=1)
+    bits = x.view(torch.int16)     # bf16 +NaN 0x7fc0, -NaN 0xffc0 set as bits
+    perm = olay.perm.view(olay.n_tiles, 128)
+    rows = [perm[t, :olay.valid_count[t]] for t in range(4)]
+    bits[rows[0][3], 0, 5] = 0x7fc0
+    bits[rows[1][0], 1, 7] = -64
+    bits[rows[2][1], 0, 9] = 0x7fc0
+    bits[rows[2][2], 0, 9] = -64
+    x[rows[3][4], 1, 11] = float('inf')
+    x[rows[3][5], 1, 11] = float('-inf')
+    assert torch.signbit(x[rows[1][0], 1, 7].float())
+    res = kernels.gather_and_pool(x.cuda(), lay, None, second=second)
+    tiles, feats = res[0], res[1]
+    ref_tiles = ot.gather_tiles(x, olay, None)
+    assert torch.equal(tiles.cpu().view(torch.int16), ref_tiles.view(torch.int16))
+    want = op.pool_tiles(ref_tiles, olay)
+    got = feats.cpu()
+    assert torch.isnan(want[0, 0, [5, 128 + 5, 256 + 5]]).all()
+    torch.testing.assert_close(got[..., 128:], want[..., 128:], rtol=0, atol=0, equal_nan=True)
+    torch.testing.assert_close(got[..., :128], want[..., :128], rtol=1e-5, atol=1e-6, equal_nan=True)
+    assert torch.equal(torch.isnan(got), torch.isnan(want))
+    assert torch.equal(kernels.pool_tiles(tiles, lay).isnan(), got.isnan().cuda())
+
+
 def test_empty_tile_pools_to_zero():
     lay, olay = _pair(helpers.small_layout())
     lay.valid_count[0] = 0

@@ -99,15 +99,26 @@ def test_segmented_blocks_have_independent_budgets():
         om.column_blocks(lay, om.Budget(ratio=0.25))
 
 
+@pytest.mark.parametrize('nan', [False, True])
 @pytest.mark.parametrize('seed', range(4))
-def test_selection_equals_torch_topk_on_distinct_scores(seed):
+def test_selection_equals_torch_topk_on_distinct_scores(seed, nan):
     """The reference's selection is torch.topk; with distinct scores the
-    oracle's stable order must give identical indices and keep flags."""
+    oracle's stable order must give identical indices and keep flags. With
+    `nan`, a third of the rows hold one NaN (either sign, so the order stays
+    defined): torch.topk ranks it above +inf and `val > -inf` never keeps
+    it; the oracle must agree."""
     lay = _layout(target_grid=(16, 8, 16), cond=(1, 16, 32))
     nv = lay.n_video_tiles
     g = torch.Generator().manual_seed(seed)
     scores = torch.rand(3, nv, lay.n_tiles, generator=g)
     assert scores.unique().numel() == scores.numel()
+    if nan:
+        hit = torch.rand(3, nv, generator=g) < 0.33
+        col = torch.randint(0, lay.n_tiles, (3, nv), generator=g)
+        sign = torch.where(torch.rand(3, nv, generator=g) < 0.5, -1.0, 1.0)
+        val = torch.copysign(torch.full((3, nv), float('nan')), sign)
+        scores.scatter_(-1, col[..., None], torch.where(hit, val, scores.gather(-1, col[..., None])[..., 0])[..., None])
+        assert torch.isnan(scores).sum() == hit.sum()
     blocks = om.column_blocks(lay, om.Budget(ratio=0.25), om.Budget(tiles=2.5))
     index, keep = om.select_video_blocks(scores, lay, blocks)
     # the same selection written with torch.topk (mask.py:251-284)
