@@ -596,6 +596,12 @@ __device__ __forceinline__ f32x16 sub_scores(const lds_u8* slot, const HFrag& f,
   return s;
 }
 
+// A hook called between the fragment reads and the products of a step (the
+// sparse walk issues the next step's loads there); the default does nothing.
+struct NoHook {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+
 // Scores of both 32-key sub-blocks of a step, as two interleaved MFMA
 // chains (each fragment read has the other chain's product to hide behind),
 // then the masks of sub-blocks with fewer than 32 valid keys.
@@ -620,6 +626,38 @@ __device__ __forceinline__ void pair_scores(const lds_u8* slot, const HFrag& fa,
     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
   }
   __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  mask_scores(sa, la, hi);
+  mask_scores(sb, lb, hi);
+}
+
+// The same products with hook(k) between them: the fragment reads of
+// product k + 2 are placed before product k and hook(k) before the reads of
+// k + 2, in program order (a hook that branches ends the scheduling region,
+// so the order is written out instead of left to scheduling hints).
+template <typename Hook>
+__device__ __forceinline__ void pair_scores_hooked(const lds_u8* slot, const HFrag& fa,
+                                                   const HFrag& fb, const WaveState& w, int la,
+                                                   int lb, int hi, f32x16& sa, f32x16& sb,
+                                                   Hook hook) {
+  typedef const __attribute__((address_space(3))) u32x4* lds_u32x4;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sa[e] = sb[e] = 0.f;
+  u32x4 ka[8], kb[8];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    ka[k] = *reinterpret_cast<lds_u32x4>(slot + fa.k[k]);
+    kb[k] = *reinterpret_cast<lds_u32x4>(slot + fb.k[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    hook(k);
+    if (k + 2 < 8) {
+      ka[k + 2] = *reinterpret_cast<lds_u32x4>(slot + fa.k[k + 2]);
+      kb[k + 2] = *reinterpret_cast<lds_u32x4>(slot + fb.k[k + 2]);
+    }
+    sa = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka[k]), w.qf[k], sa, 0, 0, 0);
+    sb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kb[k]), w.qf[k], sb, 0, 0, 0);
+  }
   mask_scores(sa, la, hi);
   mask_scores(sb, lb, hi);
 }
@@ -655,11 +693,15 @@ __device__ __forceinline__ void pack_probs(const float (&ps)[16], u32x4 (&pk)[2]
 // PAIR: the two sub-blocks' score products as interleaved chains with reads
 // ahead (pair_scores); the dense walk keeps them as two chains, which it
 // runs faster at long sequences (C5: 566 against 595 ms).
-template <bool PAIR = true>
+// qk_hook(k) runs between the score products (pair_scores_hooked).
+template <bool PAIR = true, typename QKHook = NoHook>
 __device__ __forceinline__ void sstep(const lds_u8* slot, const HFrag& fa, const HFrag& fb,
-                                      float c, int la, int lb, int hi, WaveState& w) {
+                                      float c, int la, int lb, int hi, WaveState& w,
+                                      QKHook qk_hook = {}) {
   f32x16 sa, sb;
-  if constexpr (PAIR) {
+  if constexpr (!std::is_same<QKHook, NoHook>::value) {
+    pair_scores_hooked(slot, fa, fb, w, la, lb, hi, sa, sb, qk_hook);
+  } else if constexpr (PAIR) {
     pair_scores(slot, fa, fb, w, la, lb, hi, sa, sb);
   } else {
     sa = sub_scores(slot, fa, w, la, hi);
@@ -1005,17 +1047,6 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     const float lk = p.lse_kept[head * p.lk_h + qrow * p.lk_s];
     ref2 = (lk > -INFINITY && lk < INFINITY) ? lk * 1.4426950408889634f : 0.f;
   }
-  if (MODE == kSparse) {
-    // The sparse walk loads no segment past a sub-block's valid keys, so a
-    // slot keeps whatever V rows it held there: zero both V halves once, so
-    // those rows are finite (their probabilities are exactly 0).
-#pragma unroll
-    for (int i = 0; i < 2 * kHalfBytes / (16 * kThreads2); ++i) {
-      const int off = (i * kThreads2 + tid) * 16;
-      lds_u8* dst = (lds_u8*)ring[off / kHalfBytes] + kHalfBytes + off % kHalfBytes;
-      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(dst) = u32x4{0, 0, 0, 0};
-    }
-  }
   __syncthreads();  // step list, weights, valid counts and list step count ready
   const int n_lsteps = __builtin_amdgcn_readfirstlane(step_total);
   const int n_big = LISTS ? __builtin_amdgcn_readfirstlane(step_big) : 0;
@@ -1155,8 +1186,8 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     // b of step 64 m + i of the current window m, as (first key row << 6 |
     // valid keys of the sub-block, clamped to 0 .. 32), decoded from the LDS
     // step list by all lanes at once, once per 64 steps. A step's record is
-    // read into scalar registers (v_readlane) when its loads are issued, one
-    // step ahead, and carried to its compute, so the loop itself reads no
+    // read into scalar registers (v_readlane) one step ahead, when its loads
+    // are issued, and carried to its compute, so the loop itself reads no
     // step list and waits on no LDS read for it.
     uint32_t win_a = 0, win_b = 0;
     auto lane_half = [&](int e, int64_t& r0, int& vch) {
@@ -1181,6 +1212,9 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       } else if (u < n_lsteps) {
         const int k = 2 * (u - n_big);
         lane_half(steps[2 * kMaxBlocks - 1 - k], row0, la);
+        // the last ragged half of an odd count has no partner: sub-block b
+        // loads sub-block a's rows (a kept tile), all of them masked
+        rowb = row0;
         if (k + 1 < n_small) lane_half(steps[2 * kMaxBlocks - 2 - k], rowb, lb);
       }
       win_a = ((uint32_t)row0 << 6) | (uint32_t)min(max(la, 0), 32);
@@ -1191,57 +1225,79 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       ra = (uint32_t)__builtin_amdgcn_readlane((int)win_a, u & 63);
       rb = (uint32_t)__builtin_amdgcn_readlane((int)win_b, u & 63);
     };
-    // waves 0, 1 load sub-block a, waves 2, 3 sub-block b (rows
-    // 16 (wave & 1) .. + 15 of it); a segment past the sub-block's valid
-    // keys is not loaded (its rows are masked: the scores become -inf, the
-    // probabilities exactly 0, and the slot's V rows there are finite)
-    auto load_rec = [&](uint32_t ra, uint32_t rb, lds_u8* slot) {
-      const uint32_t rec = wave < 2 ? ra : rb;
-      const int64_t base = (int64_t)(rec >> 6);
-      const int lim = (int)(rec & 63u);
-      const char* kb = reinterpret_cast<const char*>(kbase + base * p.ks);
-      const char* vb = reinterpret_cast<const char*>(vbase + base * p.vs);
+    // A step's loads: waves 0, 1 load sub-block a, waves 2, 3 sub-block b,
+    // rows 16 (wave & 1) .. + 15 of it as four 1 KB segments of K and four of
+    // V, with no branch. Segments past the sub-block's valid keys load the
+    // key tile's own padding rows, as the reference's kernel reads them (they
+    // are masked: the scores become -inf, the probabilities exactly 0); at
+    // C2 they are 0.5 % of the segments.
+    auto rec_base = [&](uint32_t ra, uint32_t rb, const char*& kb, const char*& vb) {
+      const int64_t base = (int64_t)((wave < 2 ? ra : rb) >> 6);
+      kb = reinterpret_cast<const char*>(kbase + base * p.ks);
+      vb = reinterpret_cast<const char*>(vbase + base * p.vs);
+    };
+    // load j of a step: K segment j (j < 4) or V segment j - 4, into the
+    // slot whose segment 4 wave (this wave's first) is at LDS address lds
+    auto issue = [&](const char* kb, const char* vb, int j, uint32_t lds) {
+      const int u4 = j & 3;
+      if (j < 4)
+        dma16_m0(kb, dma.k[u4], lds + u4 * 1024);
+      else
+        dma16_m0(vb, dma.v[u4], lds + kHalfBytes + u4 * 1024);
+    };
+    // this wave's first segment of each slot, as LDS addresses
+    const uint32_t lds_s0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(s0 + 4 * wave * 1024));
+    const uint32_t lds_s1 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(s1 + 4 * wave * 1024));
+    // Step (ra, rb) from `cur`, with the loads of step (na, nb) into `nxt`
+    // (unless it is the last step) issued between its products, so a load
+    // that waits for the CU's load path waits beside this wave's own running
+    // products. Issued in one burst after the barrier, the loads of all
+    // eight waves of a CU queue at the load path together and each wave
+    // stalls on them.
+    auto step = [&](auto zero, bool more, uint32_t ra, uint32_t rb, const lds_u8* cur,
+                    uint32_t na, uint32_t nb, uint32_t nxt) __attribute__((always_inline)) {
+      const int la = (int)(ra & 63u), lb = (int)(rb & 63u);
+      const char *kb, *vb;
+      rec_base(na, nb, kb, vb);
+      if constexpr (decltype(zero)::value) {
+        if (more) {
 #pragma unroll
-      for (int u4 = 0; u4 < 4; ++u4) {
-        const int seg = 4 * wave + u4;
-        if (4 * (4 * (wave & 1) + u4) < lim) {
-          dma16(kb, dma.k[u4], slot + seg * 1024);
-          dma16(vb, dma.v[u4], slot + kHalfBytes + seg * 1024);
+          for (int j = 0; j < 8; ++j) issue(kb, vb, j, nxt);
         }
+        sstep_zero_q(cur, fa, fb, la, lb, hi, w);
+      } else {
+        sstep(cur, fa, fb, c, la, lb, hi, w, [&](int k) {
+          if (more) issue(kb, vb, k, nxt);
+        });
       }
     };
-    auto compute = [&](auto zero, uint32_t ra, uint32_t rb, const lds_u8* cur)
-                       __attribute__((always_inline)) {
-      if constexpr (decltype(zero)::value)
-        sstep_zero_q(cur, fa, fb, (int)(ra & 63u), (int)(rb & 63u), hi, w);
-      else
-        sstep(cur, fa, fb, c, (int)(ra & 63u), (int)(rb & 63u), hi, w);
-    };
-    // Two copies of the loop, one per kind of wave (same loads and
-    // barriers), so each keeps O in one set of registers.
+    // Two copies of the walk, one per kind of wave (same loads and
+    // barriers), so each keeps O in one set of registers. Step u computes
+    // from slot u % 2 and loads step u + 1 into the other.
     auto walk = [&](auto zero) __attribute__((always_inline)) {
       uint32_t ca = 0, cb = 0;
       if (n_steps > 0) {
         fetch(0, ca, cb);
-        load_rec(ca, cb, s0);
+        const char *kb, *vb;
+        rec_base(ca, cb, kb, vb);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) issue(kb, vb, j, lds_s0);
       }
       for (int u = 0; u < n_steps; u += 2) {
         uint32_t na = 0, nb = 0;
         VEDA_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
-        if (u + 1 < n_steps) {
-          fetch(u + 1, na, nb);
-          load_rec(na, nb, s1);
-        }
-        compute(zero, ca, cb, s0);
-        if (u + 1 >= n_steps) break;
+        const bool more1 = u + 1 < n_steps;
+        if (more1) fetch(u + 1, na, nb);
+        step(zero, more1, ca, cb, s0, na, nb, lds_s1);
+        if (!more1) break;
         VEDA_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
-        if (u + 2 < n_steps) {
-          fetch(u + 2, ca, cb);
-          load_rec(ca, cb, s0);
-        }
-        compute(zero, na, nb, s1);
+        const bool more2 = u + 2 < n_steps;
+        if (more2) fetch(u + 2, ca, cb);
+        step(zero, more2, na, nb, s1, ca, cb, lds_s0);
       }
     };
     if (q_zero)

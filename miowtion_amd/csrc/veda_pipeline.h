@@ -81,6 +81,19 @@ __device__ __forceinline__ void dma16(const char* base, uint32_t voff, const lds
       : "memory", "m0");
 }
 
+// dma16 with the LDS destination given as its wave-uniform 32-bit LDS
+// address (the value M0 takes), e.g. a per-wave slot base in a scalar
+// register plus a constant segment offset.
+__device__ __forceinline__ void dma16_m0(const char* base, uint32_t voff, uint32_t m0) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(base), "s"(m0)
+      : "memory", "m0");
+}
+
 // Workgroup order with the last `front` tiles of every head first: block b
 // < heads * front takes (head b / front, tile n - front + b % front), the
 // other blocks the remaining tiles head by head. Tiles that a mask makes
