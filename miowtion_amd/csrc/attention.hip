@@ -662,20 +662,23 @@ __device__ __forceinline__ void pair_scores_hooked(const lds_u8* slot, const HFr
   mask_scores(sb, lb, hi);
 }
 
+// The V^T fragment (A operand) of product (kk, dt) of a sub-block: two
+// transposed reads of its 16-key group kk.
+__device__ __forceinline__ bf16x8 vt_frag(const lds_u8* slot, const HFrag& f, int kk, int dt) {
+  const lds_u8* vs = slot + kk * 16 * 256;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + f.v[dt]));
+  const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + 8 * 256 + f.v[dt]));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 __device__ __forceinline__ void sub_pv(const lds_u8* slot, const HFrag& f, const u32x4 (&pk)[2],
                                        WaveState& w) {
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    const lds_u8* vs = slot + kk * 16 * 256;
+  for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + f.v[dt]));
-      const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vs + 8 * 256 + f.v[dt]));
-      const bf16x8 a =
-          __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
-      w.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_bf16x8(pk[kk]), w.o[dt], 0, 0, 0);
-    }
-  }
+    for (int dt = 0; dt < 4; ++dt)
+      w.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vt_frag(slot, f, kk, dt), as_bf16x8(pk[kk]),
+                                                        w.o[dt], 0, 0, 0);
 }
 
 __device__ __forceinline__ void pack_probs(const float (&ps)[16], u32x4 (&pk)[2]) {
@@ -707,6 +710,7 @@ __device__ __forceinline__ void sstep(const lds_u8* slot, const HFrag& fa, const
     sa = sub_scores(slot, fa, w, la, hi);
     sb = sub_scores(slot, fb, w, lb, hi);
   }
+
   float mloc = -INFINITY;
 #pragma unroll
   for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sa[e]);
@@ -935,6 +939,21 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       dma16(vb, vo, slot + kHalfBytes + seg * 1024);
     }
   };
+  // Set-up: every independent global load goes out first (Q, the valid
+  // counts, the list counts and the lists' first entries), so the set-up
+  // waits for memory about once instead of once per dependent hop.
+  WaveState w;
+  const uint16_t* qptr = p.q + qrow * p.qs + head * p.qh;
+  bool q_live = !DENSE || qrow < p.used;
+  if (MODE == kSparse && p.seq_q != nullptr) {
+    const int64_t sh = p.seq_heads[head], src = p.seq_q[qrow];
+    q_live = p.slot_ok[qrow] != 0 && src >= 0 && src < p.seq_rows && sh >= 0 &&
+             sh < p.seq_heads_n;
+    qptr = p.q + (q_live ? src : 0) * p.qs + (q_live ? sh : 0) * p.qh;
+  }
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    w.qf[s] = q_live ? as_bf16x8(ld16(qptr + 16 * s + 8 * hi)) : as_bf16x8(u32x4{0, 0, 0, 0});
   if (VKEYS) {
     // weights of virtual keys 0 .. n_k - 1, padded with zeros to whole steps
     const uint8_t* keep_row = p.keep + (head * p.n_q_tiles + r) * p.n_k_tiles;
@@ -955,15 +974,20 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     // and are computed two to a step (one per 32-key sub-block), so no
     // step leaves a sub-block idle. Ranks come from ballots, so the order,
     // and with it the summation order, is deterministic.
-    for (int j = tid; j < nk; j += kThreads2) tvc[j] = (uint8_t)min(max(p.valid_count[j], 0), kTile);
     const int64_t li_ = head * p.n_q_tiles + r;
     const int ld = (int)p.list_ld;
-    const int nf = min(max(p.full_cnt[li_], 0), min(ld, kMaxBlocks));
-    const int np = min(max(p.part_cnt[li_], 0), min(ld, kMaxBlocks - nf));
     const int32_t* fl = p.full_idx + li_ * p.list_ld;
     const int32_t* pl = p.part_idx + li_ * p.list_ld;
+    // the first entries of both lists, loaded before their counts arrive
+    // (every row holds list_ld >= n_k entries)
+    const int32_t f0 = tid < ld ? fl[tid] : -1;
+    const int32_t p0 = tid < ld ? pl[tid] : -1;
+    const int nf = min(max(p.full_cnt[li_], 0), min(ld, kMaxBlocks));
+    const int np = min(max(p.part_cnt[li_], 0), min(ld, kMaxBlocks - nf));
+    for (int j = tid; j < nk; j += kThreads2) tvc[j] = (uint8_t)min(max(p.valid_count[j], 0), kTile);
+    __syncthreads();  // valid counts in LDS
     for (int i = tid; i < nf; i += kThreads2) {
-      const int32_t j = fl[i];
+      const int32_t j = i < kThreads2 ? f0 : fl[i];
       const bool ok = j >= 0 && j < nk;
       steps[2 * i] = ok ? (uint16_t)((j << 2) | 1) : kVoidStep;
       steps[2 * i + 1] = ok ? (uint16_t)((j << 2) | 3) : kVoidStep;
@@ -976,9 +1000,9 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
         int32_t j = -1;
         bool ok = false;
         if (i < np) {
-          j = pl[i];
+          j = i0 == 0 ? p0 : pl[i];
           ok = j >= 0 && j < nk;
-          if (ok) vc = min(max(p.valid_count[j], 0), kTile);
+          if (ok) vc = tvc[j];
         }
         // an entry outside [0, n_k) or a tile with no valid key: one void
         // step, as a full-list entry outside [0, n_k) is
@@ -1008,18 +1032,6 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     }
   }
 
-  WaveState w;
-  const uint16_t* qptr = p.q + qrow * p.qs + head * p.qh;
-  bool q_live = !DENSE || qrow < p.used;
-  if (MODE == kSparse && p.seq_q != nullptr) {
-    const int64_t sh = p.seq_heads[head], src = p.seq_q[qrow];
-    q_live = p.slot_ok[qrow] != 0 && src >= 0 && src < p.seq_rows && sh >= 0 &&
-             sh < p.seq_heads_n;
-    qptr = p.q + (q_live ? src : 0) * p.qs + (q_live ? sh : 0) * p.qh;
-  }
-#pragma unroll
-  for (int s = 0; s < 8; ++s)
-    w.qf[s] = q_live ? as_bf16x8(ld16(qptr + 16 * s + 8 * hi)) : as_bf16x8(u32x4{0, 0, 0, 0});
 #pragma unroll
   for (int s = 0; s < 8; ++s) asm volatile("" : : "v"(w.qf[s]));
   // a wave whose 32 query rows are all zero (padding rows) takes the
@@ -1409,15 +1421,26 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   asm volatile("" ::: "memory");
   const uint64_t orow_bits = reinterpret_cast<uintptr_t>(orow);
   const bool row16 = ((p.os | p.oh) & 7) == 0;  // every row start 16-byte aligned
+  // rows in sequence order come from the lane that owns the row; otherwise
+  // row rr of this wave's 32 is at a fixed stride
+  const bool seq_rows = MODE == kSparse && p.seq_o != nullptr;
+  uint16_t* const wave_rows = p.out + (r * kTile + 32 * wave) * p.os + head * p.oh;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int rr = 4 * i + (lane >> 4), ch = lane & 15;
-    const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)orow_bits, rr);
-    const uint32_t up = (uint32_t)__shfl((int)(uint32_t)(orow_bits >> 32), rr);
-    const bool live = __shfl((int)o_live, rr) != 0;
     const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
         stage + rr * 256 + ((ch ^ (rr & 15)) << 4));
-    uint16_t* dst = reinterpret_cast<uint16_t*>((uintptr_t)(((uint64_t)up << 32) | lo)) + 8 * ch;
+    uint16_t* dst;
+    bool live;
+    if (seq_rows) {
+      const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)orow_bits, rr);
+      const uint32_t up = (uint32_t)__shfl((int)(uint32_t)(orow_bits >> 32), rr);
+      live = __shfl((int)o_live, rr) != 0;
+      dst = reinterpret_cast<uint16_t*>((uintptr_t)(((uint64_t)up << 32) | lo)) + 8 * ch;
+    } else {
+      live = !DENSE || r * kTile + 32 * wave + rr < p.q_rows;
+      dst = wave_rows + rr * p.os + 8 * ch;
+    }
     if (live) {
       if (row16) {
         *reinterpret_cast<u32x4*>(dst) = v;
