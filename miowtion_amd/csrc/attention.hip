@@ -900,6 +900,10 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   // virtual keys: per key tile, its real row count if dropped, else 0
   __shared__ __attribute__((aligned(16))) uint8_t vwt[VKEYS ? kMaxBlocks + kHalf : 4];
   __shared__ int32_t step_total, step_big, step_small;
+  // sparse walk: which waves' 32 query rows are all zero, and the LSE of
+  // their rows (all alike; see the copy waves below)
+  __shared__ uint8_t zflag[4];
+  __shared__ float zero_lse;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 31, hi = lane >> 5;
@@ -1045,6 +1049,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       any |= x[0] | x[1] | x[2] | x[3];
     }
     q_zero = __ballot(any != 0) == 0;
+    if (lane == 0) zflag[wave] = q_zero ? 1 : 0;
   }
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -1060,6 +1065,20 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     ref2 = (lk > -INFINITY && lk < INFINITY) ? lk * 1.4426950408889634f : 0.f;
   }
   __syncthreads();  // step list, weights, valid counts and list step count ready
+  // All-zero query groups of one tile have the same output and LSE (the
+  // uniform average over the tile's valid kept keys, the same products in
+  // the same order): the first such wave computes it, the others ("copy"
+  // waves) only load and pass the barriers, then store its staged rows.
+  int zero_src = 0;
+  bool copy = false, has_copy = false;  // has_copy: workgroup-uniform
+  if (MODE == kSparse) {
+    const uint32_t zbits = __builtin_amdgcn_readfirstlane(
+        (uint32_t)zflag[0] | ((uint32_t)zflag[1] << 1) | ((uint32_t)zflag[2] << 2) |
+        ((uint32_t)zflag[3] << 3));
+    zero_src = zbits ? __builtin_ctz(zbits) : 0;
+    copy = q_zero && wave != zero_src;
+    has_copy = __builtin_popcount(zbits) >= 2;
+  }
   const int n_lsteps = __builtin_amdgcn_readfirstlane(step_total);
   const int n_big = LISTS ? __builtin_amdgcn_readfirstlane(step_big) : 0;
   const int n_small = LISTS ? __builtin_amdgcn_readfirstlane(step_small) : 0;
@@ -1268,26 +1287,28 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     // products. Issued in one burst after the barrier, the loads of all
     // eight waves of a CU queue at the load path together and each wave
     // stalls on them.
-    auto step = [&](auto zero, bool more, uint32_t ra, uint32_t rb, const lds_u8* cur,
+    // kind: 0 a wave with a real query row, 1 the wave that computes the
+    // all-zero groups' output, 2 a copy wave (loads only)
+    auto step = [&](auto kind, bool more, uint32_t ra, uint32_t rb, const lds_u8* cur,
                     uint32_t na, uint32_t nb, uint32_t nxt) __attribute__((always_inline)) {
       const int la = (int)(ra & 63u), lb = (int)(rb & 63u);
       const char *kb, *vb;
       rec_base(na, nb, kb, vb);
-      if constexpr (decltype(zero)::value) {
+      if constexpr (decltype(kind)::value != 0) {
         if (more) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) issue(kb, vb, j, nxt);
         }
-        sstep_zero_q(cur, fa, fb, la, lb, hi, w);
+        if constexpr (decltype(kind)::value == 1) sstep_zero_q(cur, fa, fb, la, lb, hi, w);
       } else {
         sstep(cur, fa, fb, c, la, lb, hi, w, [&](int k) {
           if (more) issue(kb, vb, k, nxt);
         });
       }
     };
-    // Two copies of the walk, one per kind of wave (same loads and
-    // barriers), so each keeps O in one set of registers. Step u computes
-    // from slot u % 2 and loads step u + 1 into the other.
+    // A copy of the walk per kind of wave (same loads and barriers), so
+    // each keeps O in one set of registers. Step u computes from slot u % 2
+    // and loads step u + 1 into the other.
     auto walk = [&](auto zero) __attribute__((always_inline)) {
       uint32_t ca = 0, cb = 0;
       if (n_steps > 0) {
@@ -1312,10 +1333,12 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
         step(zero, more2, na, nb, s1, ca, cb, lds_s0);
       }
     };
-    if (q_zero)
-      walk(std::true_type{});
+    if (copy)
+      walk(std::integral_constant<int, 2>{});
+    else if (q_zero)
+      walk(std::integral_constant<int, 1>{});
     else
-      walk(std::false_type{});
+      walk(std::integral_constant<int, 0>{});
   } else {
   if (n_steps > 0) load_step(0, s0);
   if (!VKEYS) {
@@ -1393,31 +1416,44 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   lds_u8* stage = (lds_u8*)ring[n_steps & 1] + wave * 8192;
   if (kept_lds) VEDA_WAIT_VM(0);  // this wave's o_kept rows are in its part of `stage`
+  if (!copy) {
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int e = 4 * g;
-      const int d = 32 * dt + 8 * g + 4 * hi;
-      float kept4[4] = {0.f, 0.f, 0.f, 0.f};
-      if (MODE == kVirtualOnly) {
-        const u32x2 kv =
-            kept_lds ? *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(
-                           stage + li * 256 + (((4 * dt + g) ^ (li & 15)) << 4) + 8 * hi)
-                     : *reinterpret_cast<const u32x2*>(krow + d);
-        kept4[0] = bf16_to_f32(kv[0] & 0xffffu);
-        kept4[1] = bf16_to_f32(kv[0] >> 16);
-        kept4[2] = bf16_to_f32(kv[1] & 0xffffu);
-        kept4[3] = bf16_to_f32(kv[1] >> 16);
+      for (int g = 0; g < 4; ++g) {
+        const int e = 4 * g;
+        const int d = 32 * dt + 8 * g + 4 * hi;
+        float kept4[4] = {0.f, 0.f, 0.f, 0.f};
+        if (MODE == kVirtualOnly) {
+          const u32x2 kv =
+              kept_lds ? *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(
+                             stage + li * 256 + (((4 * dt + g) ^ (li & 15)) << 4) + 8 * hi)
+                       : *reinterpret_cast<const u32x2*>(krow + d);
+          kept4[0] = bf16_to_f32(kv[0] & 0xffffu);
+          kept4[1] = bf16_to_f32(kv[0] >> 16);
+          kept4[2] = bf16_to_f32(kv[1] & 0xffffu);
+          kept4[3] = bf16_to_f32(kv[1] >> 16);
+        }
+        float v4[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          v4[m] = (MODE == kVirtualOnly ? kept4[m] + w.o[dt][e + m] : w.o[dt][e + m]) * inv;
+        const uint32_t w0 = pack_bf16x2(v4[0], v4[1]), w1 = pack_bf16x2(v4[2], v4[3]);
+        *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(
+            stage + li * 256 + (((4 * dt + g) ^ (li & 15)) << 4) + 8 * hi) = u32x2{w0, w1};
       }
-      float v4[4];
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        v4[m] = (MODE == kVirtualOnly ? kept4[m] + w.o[dt][e + m] : w.o[dt][e + m]) * inv;
-      const uint32_t w0 = pack_bf16x2(v4[0], v4[1]), w1 = pack_bf16x2(v4[2], v4[3]);
-      *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(
-          stage + li * 256 + (((4 * dt + g) ^ (li & 15)) << 4) + 8 * hi) = u32x2{w0, w1};
+  }
+  float lse_val = !row_real ? 0.f : l > 0.f ? (w.m_run + __log2f(l)) * kLn2 : -INFINITY;
+  const lds_u8* src = stage;
+  if (has_copy) {
+    // copy waves store the rows (and LSE) the first all-zero wave staged
+    if (wave == zero_src && lane == 0) zero_lse = lse_val;
+    __syncthreads();
+    if (copy) {
+      src = (const lds_u8*)ring[n_steps & 1] + zero_src * 8192;
+      lse_val = zero_lse;
     }
+  }
   asm volatile("" ::: "memory");
   const uint64_t orow_bits = reinterpret_cast<uintptr_t>(orow);
   const bool row16 = ((p.os | p.oh) & 7) == 0;  // every row start 16-byte aligned
@@ -1429,7 +1465,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   for (int i = 0; i < 8; ++i) {
     const int rr = 4 * i + (lane >> 4), ch = lane & 15;
     const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
-        stage + rr * 256 + ((ch ^ (rr & 15)) << 4));
+        src + rr * 256 + ((ch ^ (rr & 15)) << 4));
     uint16_t* dst;
     bool live;
     if (seq_rows) {
@@ -1451,8 +1487,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     }
   }
   if ((MODE == kSparse || DENSE) && p.lse != nullptr && hi == 0 && row_exists)
-    p.lse[head * p.lse_sh + qrow * p.lse_ss] =
-        !row_real ? 0.f : l > 0.f ? (w.m_run + __log2f(l)) * kLn2 : -INFINITY;
+    p.lse[head * p.lse_sh + qrow * p.lse_ss] = lse_val;
 }
 
 // ---------------------------------------------------------------------------
