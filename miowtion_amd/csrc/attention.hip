@@ -800,28 +800,98 @@ __device__ __forceinline__ void sub_weights(const uint8_t* wt, int key0, int hi,
 // carry weight 0); then per sub-block p = exp2(s c - ref2) where the tile's
 // weight (its real row count if dropped, else 0) is positive, den += p *
 // weight, and O^T += V^T P^T, sub-block a's terms before b's.
+//
+// With the reference fixed, nothing of sub-block a waits for b's scores (no
+// running max), so the step is software-pipelined: a's score products; b's
+// score products with a's probabilities (vector unit) between them; a's
+// P·V products with b's probabilities between them; b's P·V products. The
+// matrix and vector units then work at once inside the wave instead of in
+// turn. Every accumulator sees the same products in the same order as the
+// plain sequence (a's scores, b's, a's P·V, b's), so the result is the
+// same bit for bit.
 __device__ __forceinline__ void vstep_fixed(const lds_u8* slot, const HFrag& fa, const HFrag& fb,
                                             float c, const uint8_t* wt, int key0, int hi,
                                             float ref2, WaveState& w) {
-  f32x16 sa, sb;
-  pair_scores(slot, fa, fb, w, 32, 32, hi, sa, sb);
-  auto probs = [&](const f32x16& s, int k0, u32x4 (&pk)[2]) {
-    float ww[16], ps[16], den = 0.f;
-    sub_weights(wt, k0, hi, ww);
+  typedef const __attribute__((address_space(3))) u32x4* lds_u32x4;
+  // The order is written out, one product and its companions per stage,
+  // with scheduling fences between the stages.
+#define VEDA_FENCE() __builtin_amdgcn_sched_barrier(0)
+  auto kread = [&](const HFrag& f, int k) { return *reinterpret_cast<lds_u32x4>(slot + f.k[k]); };
+  // weights stay packed, four per word (byte m of word g is key 8 g + 4 hi + m)
+  uint32_t wa[4], wb[4];
+  auto wread = [&](int k0, uint32_t (&wp)[4]) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float x = ww[e] > 0.f ? __builtin_amdgcn_exp2f(fmaf(s[e], c, -ref2)) : 0.f;
-      ps[e] = x;
-      den = fmaf(x, ww[e], den);
-    }
-    w.l_run += den;
-    pack_probs(ps, pk);
+    for (int g = 0; g < 4; ++g) wp[g] = *reinterpret_cast<const uint32_t*>(wt + k0 + 8 * g + 4 * hi);
   };
-  u32x4 ka[2], kb[2];
-  probs(sa, key0, ka);
-  probs(sb, key0 + 32, kb);
-  sub_pv(slot, fa, ka, w);
-  sub_pv(slot, fb, kb, w);
+  f32x16 sa, sb;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sa[e] = sb[e] = 0.f;
+  u32x4 ka[8], kb[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ka[k] = kread(fa, k);
+  VEDA_FENCE();
+  // a's score products, K fragments read four ahead
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    sa = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka[k]), w.qf[k], sa, 0, 0, 0);
+    if (k < 4) ka[k + 4] = kread(fa, k + 4);
+    else kb[k - 4] = kread(fb, k - 4);
+    if (k == 0) wread(key0, wa);
+    if (k == 1) wread(key0 + 32, wb);
+    VEDA_FENCE();
+  }
+  // one sub-block's probabilities in eight pieces of two keys each (den
+  // summed in key order, as in one pass)
+  float den = 0.f;
+  float ps[2];
+  auto piece = [&](const f32x16& s, const uint32_t (&wp)[4], int k, u32x4 (&pk)[2]) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int e = 2 * k + m;
+      const float ww = (float)((wp[e >> 2] >> (8 * (e & 3))) & 0xffu);
+      const float x = ww > 0.f ? __builtin_amdgcn_exp2f(fmaf(s[e], c, -ref2)) : 0.f;
+      ps[m] = x;
+      den = fmaf(x, ww, den);
+    }
+    pk[k >> 2][k & 3] = pack_bf16x2(ps[0], ps[1]);
+  };
+  // b's score products with a's probabilities; a's first V^T fragments
+  u32x4 pa[2], pb[2];
+  bf16x8 va[2][4], vb[2][4];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    sb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kb[k]), w.qf[k], sb, 0, 0, 0);
+    if (k < 4) kb[k + 4] = kread(fb, k + 4);
+    else if (k < 6) va[0][k - 4] = vt_frag(slot, fa, 0, k - 4);
+    piece(sa, wa, k, pa);
+    VEDA_FENCE();
+  }
+  w.l_run += den;
+  den = 0.f;
+  // a's P.V products with b's probabilities, V^T fragments two ahead
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int kk = j >> 2, dt = j & 3;
+    w.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[kk][dt], as_bf16x8(pa[kk]), w.o[dt], 0,
+                                                      0, 0);
+    const int n = j + 2;
+    if (n < 8) va[n >> 2][n & 3] = vt_frag(slot, fa, n >> 2, n & 3);
+    else vb[0][n - 8] = vt_frag(slot, fb, 0, n - 8);
+    piece(sb, wb, j, pb);
+    VEDA_FENCE();
+  }
+  w.l_run += den;
+  // b's P.V products
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int kk = j >> 2, dt = j & 3;
+    w.o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb[kk][dt], as_bf16x8(pb[kk]), w.o[dt], 0,
+                                                      0, 0);
+    const int n = j + 2;
+    if (n < 8) vb[n >> 2][n & 3] = vt_frag(slot, fb, n >> 2, n & 3);
+    VEDA_FENCE();
+  }
+#undef VEDA_FENCE
 }
 
 // One step of 64 virtual keys inside the online softmax (compensated
@@ -958,13 +1028,34 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
 #pragma unroll
   for (int s = 0; s < 8; ++s)
     w.qf[s] = q_live ? as_bf16x8(ld16(qptr + 16 * s + 8 * hi)) : as_bf16x8(u32x4{0, 0, 0, 0});
+  // compensation of a given output: the row's lse_kept, and the first
+  // virtual step, which depends on nothing the set-up computes
+  float lk = 0.f;
+  if (MODE == kVirtualOnly) {
+    lk = p.lse_kept[head * p.lk_h + qrow * p.lk_s];
+    load_virtual(0, (lds_u8*)ring[0]);
+  }
   if (VKEYS) {
-    // weights of virtual keys 0 .. n_k - 1, padded with zeros to whole steps
+    // weights of virtual keys 0 .. n_k - 1, padded with zeros to whole
+    // steps, four per thread and word; both loads of an entry are issued
+    // whatever its keep flag (indices clamped to n_k - 1), so the set-up
+    // waits for memory once per pass instead of once per dependent load
     const uint8_t* keep_row = p.keep + (head * p.n_q_tiles + r) * p.n_k_tiles;
-    for (int j = tid; j < n_virt * kHalf; j += kThreads2) {
-      int wj = 0;
-      if (j < nk && keep_row[j] == 0) wj = min(max(p.valid_count[j], 0), kTile);
-      vwt[j] = (uint8_t)wj;
+    for (int j4 = 4 * tid; j4 < n_virt * kHalf; j4 += 4 * kThreads2) {
+      int kp[4], vn[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int jj = min(j4 + m, nk - 1);
+        kp[m] = keep_row[jj];
+        vn[m] = p.valid_count[jj];
+      }
+      uint32_t packed = 0;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int wj = (j4 + m < nk && kp[m] == 0) ? min(max(vn[m], 0), kTile) : 0;
+        packed |= (uint32_t)wj << (8 * m);
+      }
+      *reinterpret_cast<uint32_t*>(vwt + j4) = packed;
     }
   }
   if (!LISTS) {
@@ -1059,11 +1150,8 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   w.l_run = 0.f;
   // compensation of a given output: the row's fixed reference (0 for a row
   // that kept nothing)
-  float ref2 = 0.f;
-  if (MODE == kVirtualOnly) {
-    const float lk = p.lse_kept[head * p.lk_h + qrow * p.lk_s];
-    ref2 = (lk > -INFINITY && lk < INFINITY) ? lk * 1.4426950408889634f : 0.f;
-  }
+  const float ref2 =
+      MODE == kVirtualOnly && lk > -INFINITY && lk < INFINITY ? lk * 1.4426950408889634f : 0.f;
   __syncthreads();  // step list, weights, valid counts and list step count ready
   // All-zero query groups of one tile have the same output and LSE (the
   // uniform average over the tile's valid kept keys, the same products in
@@ -1340,7 +1428,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     else
       walk(std::integral_constant<int, 0>{});
   } else {
-  if (n_steps > 0) load_step(0, s0);
+  if (n_steps > 0 && MODE != kVirtualOnly) load_step(0, s0);  // kVirtualOnly: issued at set-up
   if (!VKEYS) {
     for (int u = 0; u < n_steps; u += 2) {
       begin_step(u, s1);
@@ -1417,22 +1505,36 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   lds_u8* stage = (lds_u8*)ring[n_steps & 1] + wave * 8192;
   if (kept_lds) VEDA_WAIT_VM(0);  // this wave's o_kept rows are in its part of `stage`
   if (!copy) {
+    // compensation: all 16 pieces of o_kept are read before any is used
+    // (one wait instead of one per piece)
+    u32x2 kv[4][4];
+    if (MODE == kVirtualOnly) {
+      if (kept_lds) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            kv[dt][g] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(
+                stage + li * 256 + (((4 * dt + g) ^ (li & 15)) << 4) + 8 * hi);
+      } else {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            kv[dt][g] = *reinterpret_cast<const u32x2*>(krow + 32 * dt + 8 * g + 4 * hi);
+      }
+    }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int e = 4 * g;
-        const int d = 32 * dt + 8 * g + 4 * hi;
         float kept4[4] = {0.f, 0.f, 0.f, 0.f};
         if (MODE == kVirtualOnly) {
-          const u32x2 kv =
-              kept_lds ? *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(
-                             stage + li * 256 + (((4 * dt + g) ^ (li & 15)) << 4) + 8 * hi)
-                       : *reinterpret_cast<const u32x2*>(krow + d);
-          kept4[0] = bf16_to_f32(kv[0] & 0xffffu);
-          kept4[1] = bf16_to_f32(kv[0] >> 16);
-          kept4[2] = bf16_to_f32(kv[1] & 0xffffu);
-          kept4[3] = bf16_to_f32(kv[1] >> 16);
+          kept4[0] = bf16_to_f32(kv[dt][g][0] & 0xffffu);
+          kept4[1] = bf16_to_f32(kv[dt][g][0] >> 16);
+          kept4[2] = bf16_to_f32(kv[dt][g][1] & 0xffffu);
+          kept4[3] = bf16_to_f32(kv[dt][g][1] >> 16);
         }
         float v4[4];
 #pragma unroll
