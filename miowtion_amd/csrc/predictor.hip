@@ -2,10 +2,17 @@
 // block logits (q_hat k_hat^T / sqrt(D) + optional terms), fp32 throughout
 // as in the reference (miowtion/veda/predictor.py:251-338).
 //
-// Both are 64x64-output LDS-tiled fp32 GEMMs (256 threads, 4x4 outputs per
-// thread, k-chunks of 16). The weights are decoded in the load path: bf16,
-// fp32, or fp8 e4m3 with a per-head scale, turned into the resident bf16
-// value bf16(e4m3 * scale) of miowtion/veda/bundle.py:280-297 before use.
+// Both run on the matrix cores in fp32 (v_mfma_f32_32x32x2_f32: exact
+// products, fp32 sums, as a fp32 GEMM): 64x64 outputs per workgroup, 32x32
+// per wave, operands staged through LDS k-contiguous. The MFMA sums over
+// its two k in any order, so lane half g supplies k = k0 + 4 g + j to
+// product j of a chunk of eight, and each lane reads its four k of A and
+// of B as one 16-byte LDS read. The
+// weights are decoded in the load path: bf16, fp32, or fp8 e4m3 with a
+// per-head scale, turned into the resident bf16 value bf16(e4m3 * scale) of
+// miowtion/veda/bundle.py:280-297 before use. Shapes whose k is not a
+// multiple of 4, or rows that are not 16-byte aligned, take the
+// LDS-tiled VALU form (64x64 outputs, 4x4 per thread, k-chunks of 16).
 
 #include "veda_common.h"
 
@@ -145,6 +152,159 @@ __global__ void __launch_bounds__(256) logits_kernel(
   }
 }
 
+// C[h][m][n] = sum_k A[h][m][k] B[h][k][n] on the matrix cores.
+// EMBED: A = feats [H'][M][K], B = the head's projection [K][N] (decoded),
+// plus the residual A[m][n] when asked; otherwise (logits) B[k][n] =
+// b[h][n][k] (k_hat, k-contiguous), then scale, the count term and the
+// accumulation into out.
+struct PGemm {
+  const float* a;
+  const float* b;      // logits: k_hat
+  const void* w;       // embed: projections
+  int w_dtype;
+  const float* w_scale;
+  int64_t w_heads;
+  const int64_t* heads;
+  int64_t m, n, k;
+  int residual;
+  float scale;
+  const float* gain;
+  const float* log_count;
+  int accumulate;
+  float* out;
+};
+
+constexpr int kKB = 32;       // k per staged block
+constexpr int kRow = kKB + 4; // LDS row pitch (floats)
+
+// Workgroup: 64 x 64 outputs, 4 waves of 32 x 32. Per block of 32 k, A's 64
+// rows and B's 64 columns go to LDS k-contiguous ([row][k], B transposed:
+// [n][k]) with coalesced 16-byte loads (the projection is decoded on the
+// way); the next block's loads are in flight while the current block's 16
+// products per wave run from LDS. Rows and columns past the matrix are
+// staged from clamped real rows and not stored.
+template <bool EMBED>
+__global__ void __launch_bounds__(256) pgemm_kernel(PGemm p) {
+  __shared__ __attribute__((aligned(16))) float As[2][kBM][kRow];
+  __shared__ __attribute__((aligned(16))) float Bs[2][kBN][kRow];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int li = lane & 31, g = lane >> 5;
+  const int64_t hp = blockIdx.z;
+  const int64_t mb = (int64_t)blockIdx.y * kBM, nb = (int64_t)blockIdx.x * kBN;
+  const int wm = 32 * (wave >> 1), wn = 32 * (wave & 1);
+  int64_t head = 0;
+  bool head_ok = true;
+  float wscale = 1.f;
+  if (EMBED) {
+    head = p.heads[hp];
+    head_ok = head >= 0 && head < p.w_heads;
+    if (!head_ok) head = 0;
+    wscale = (p.w_dtype == 2 && head_ok) ? p.w_scale[head] : 1.f;
+  }
+  const int64_t wbase = head * p.k * p.n;
+  // staging: thread t moves k 4 (t % 8) .. + 3 of rows t / 8 and t / 8 + 32
+  // of A (and of k_hat); for the projection, k t / 8 of columns 8 (t % 8) ..
+  // + 7
+  const int sr = tid >> 3, sk = 4 * (tid & 7);
+  struct Stage {
+    f32x4 a[2], b[2];
+    float w[8];
+  };
+  auto load = [&](Stage& st, int64_t k0) {
+    f32x4 (&ra)[2] = st.a;
+    f32x4 (&rb)[2] = st.b;
+    float (&rw)[8] = st.w;
+    const int64_t kk = k0 + sk;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t gm = min(mb + sr + 32 * h, p.m - 1);
+      ra[h] = kk < p.k ? *reinterpret_cast<const f32x4*>(p.a + (hp * p.m + gm) * p.k + kk)
+                       : f32x4{0.f, 0.f, 0.f, 0.f};
+      if (!EMBED) {
+        const int64_t gn = min(nb + sr + 32 * h, p.n - 1);
+        rb[h] = kk < p.k ? *reinterpret_cast<const f32x4*>(p.b + (hp * p.n + gn) * p.k + kk)
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    if (EMBED) {
+      const int64_t wk = k0 + sr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t gn = nb + 8 * (tid & 7) + j;
+        rw[j] = (wk < p.k && gn < p.n && head_ok) ? load_w(p.w, p.w_dtype, wbase + wk * p.n + gn, wscale)
+                                                 : 0.f;
+      }
+    }
+  };
+  auto store = [&](const Stage& st, int buf) {
+    const f32x4 (&ra)[2] = st.a;
+    const f32x4 (&rb)[2] = st.b;
+    const float (&rw)[8] = st.w;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      *reinterpret_cast<f32x4*>(&As[buf][sr + 32 * h][sk]) = ra[h];
+      if (!EMBED) *reinterpret_cast<f32x4*>(&Bs[buf][sr + 32 * h][sk]) = rb[h];
+    }
+    if (EMBED) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Bs[buf][8 * (tid & 7) + j][sr] = rw[j];
+    }
+  };
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  const int nblk = (int)((p.k + kKB - 1) / kKB);
+  auto products = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < kKB / 8; ++c) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&As[buf][wm + li][8 * c + 4 * g]);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(&Bs[buf][wn + li][8 * c + 4 * g]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j], b[j], acc, 0, 0, 0);
+    }
+  };
+  // blocks b + 1 and b + 2 are in registers or in flight while block b is
+  // in LDS being multiplied: the loads run two blocks ahead of their use
+  Stage r0, r1;
+  load(r0, 0);
+  store(r0, 0);
+  load(r0, kKB);           // block 1 (zeros past k)
+  load(r1, 2 * kKB);       // block 2
+  __syncthreads();
+  for (int kb = 0; kb < nblk; kb += 2) {
+    products(0);
+    if (kb + 1 >= nblk) break;
+    store(r0, 1);          // block kb + 1
+    load(r0, (int64_t)(kb + 3) * kKB);
+    __syncthreads();
+    products(1);
+    if (kb + 2 >= nblk) break;
+    store(r1, 0);          // block kb + 2
+    load(r1, (int64_t)(kb + 4) * kKB);
+    __syncthreads();
+  }
+  // lane (li, g) holds column nb + wn + li, rows mb + wm + 8 (e / 4) + 4 g + e % 4
+  const int64_t gn = nb + wn + li;
+  if (gn >= p.n) return;
+  float gterm = 0.f;
+  if (!EMBED && p.gain != nullptr) gterm = p.gain[p.heads[hp]] * p.log_count[gn];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int64_t gm = mb + wm + 8 * (e >> 2) + 4 * g + (e & 3);
+    if (gm >= p.m) continue;
+    const int64_t o = (hp * p.m + gm) * p.n + gn;
+    float v = acc[e];
+    if (EMBED) {
+      if (p.residual) v += p.a[(hp * p.m + gm) * p.k + gn];
+    } else {
+      v = v * p.scale;
+      if (p.gain != nullptr) v += gterm;
+      if (p.accumulate) v = p.out[o] + v;
+    }
+    p.out[o] = v;
+  }
+}
+
 }  // namespace
 }  // namespace veda
 
@@ -163,8 +323,16 @@ extern "C" int veda_predictor_embed(const float* feats, int64_t n_heads, int64_t
   dim3 grid((unsigned)((n_out + kBN - 1) / kBN), (unsigned)((n_tiles + kBM - 1) / kBM),
             (unsigned)n_heads);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  embed_kernel<<<grid, 256, 0, s>>>(feats, n_tiles, k_dim, w, w_dtype, w_scale, w_heads, heads,
-                                    n_out, residual, out);
+  if (k_dim % 4 == 0 && (reinterpret_cast<uintptr_t>(feats) & 15) == 0) {
+    PGemm p{};
+    p.a = feats; p.w = w; p.w_dtype = w_dtype; p.w_scale = w_scale; p.w_heads = w_heads;
+    p.heads = heads; p.m = n_tiles; p.n = n_out; p.k = k_dim; p.residual = residual;
+    p.out = out;
+    pgemm_kernel<true><<<grid, 256, 0, s>>>(p);
+  } else {
+    embed_kernel<<<grid, 256, 0, s>>>(feats, n_tiles, k_dim, w, w_dtype, w_scale, w_heads, heads,
+                                      n_out, residual, out);
+  }
   return check_launch("veda_predictor_embed");
 }
 
@@ -179,7 +347,14 @@ extern "C" int veda_predictor_logits(const float* a, const float* b, int64_t n_h
   dim3 grid((unsigned)((n_k + kBN - 1) / kBN), (unsigned)((n_q + kBM - 1) / kBM),
             (unsigned)n_heads);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  logits_kernel<<<grid, 256, 0, s>>>(a, b, n_q, n_k, dim, scale, gain, heads, log_count,
-                                     accumulate, out);
+  if (dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0) {
+    PGemm p{};
+    p.a = a; p.b = b; p.heads = heads; p.m = n_q; p.n = n_k; p.k = dim; p.scale = scale;
+    p.gain = gain; p.log_count = log_count; p.accumulate = accumulate; p.out = out;
+    pgemm_kernel<false><<<grid, 256, 0, s>>>(p);
+  } else {
+    logits_kernel<<<grid, 256, 0, s>>>(a, b, n_q, n_k, dim, scale, gain, heads, log_count,
+                                       accumulate, out);
+  }
   return check_launch("veda_predictor_logits");
 }
