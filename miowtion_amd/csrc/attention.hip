@@ -988,30 +988,30 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   // halves of the slot); in the last step rows past n_k do not exist, so
   // every lane reads a row below the step's count (the extra rows carry
   // weight 0).
-  auto load_virtual = [&](int v, lds_u8* slot) {
+  // load j of virtual step v: this wave's K segment j (j < 4) or V segment
+  // j - 4
+  auto virtual_seg = [&](int v, lds_u8* slot, int j) {
     const int64_t row0 = (int64_t)v * kHalf;
     const int vch = min(nk - v * kHalf, kHalf);
     const char* kb = reinterpret_cast<const char*>(p.kc + head * p.ch + row0 * p.cs);
     const char* vb = reinterpret_cast<const char*>(p.vc + head * p.ch + row0 * p.cs);
+    const int u4 = j & 3, seg = 4 * wave + u4;
+    lds_u8* dst = slot + (j < 4 ? 0 : kHalfBytes) + seg * 1024;
     if (vch == kHalf) {
       // cdma's offsets of waves 2, 3 count from row 32
       const int64_t sb = wave >= 2 ? 32 * p.cs * 2 : 0;
-#pragma unroll
-      for (int u4 = 0; u4 < 4; ++u4) {
-        dma16(kb + sb, cdma.k[u4], slot + (4 * wave + u4) * 1024);
-        dma16(vb + sb, cdma.v[u4], slot + kHalfBytes + (4 * wave + u4) * 1024);
-      }
+      dma16((j < 4 ? kb : vb) + sb, j < 4 ? cdma.k[u4] : cdma.v[u4], dst);
       return;
     }
     const int lr = lane >> 4, pc = lane & 15;
+    const int row = 4 * seg + lr, src = min(row, vch - 1);
+    const uint32_t off = j < 4 ? (uint32_t)((src * p.cs + ((pc ^ (row & 15)) << 3)) * 2)
+                               : (uint32_t)((src * p.cs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
+    dma16(j < 4 ? kb : vb, off, dst);
+  };
+  auto load_virtual = [&](int v, lds_u8* slot) {
 #pragma unroll
-    for (int u4 = 0; u4 < 4; ++u4) {
-      const int seg = 4 * wave + u4, row = 4 * seg + lr, src = min(row, vch - 1);
-      const uint32_t ko = (uint32_t)((src * p.cs + ((pc ^ (row & 15)) << 3)) * 2);
-      const uint32_t vo = (uint32_t)((src * p.cs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
-      dma16(kb, ko, slot + seg * 1024);
-      dma16(vb, vo, slot + kHalfBytes + seg * 1024);
-    }
+    for (int j = 0; j < 8; ++j) virtual_seg(v, slot, j);
   };
   // Set-up: every independent global load goes out first (Q, the valid
   // counts, the list counts and the lists' first entries), so the set-up
@@ -1132,7 +1132,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   // a wave whose 32 query rows are all zero (padding rows) takes the
   // product-free step (wave-uniform)
   bool q_zero = false;
-  if (MODE == kSparse) {
+  if (MODE == kSparse || MODE == kSparseComp) {
     uint32_t any = 0;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
@@ -1140,7 +1140,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       any |= x[0] | x[1] | x[2] | x[3];
     }
     q_zero = __ballot(any != 0) == 0;
-    if (lane == 0) zflag[wave] = q_zero ? 1 : 0;
+    if (MODE == kSparse && lane == 0) zflag[wave] = q_zero ? 1 : 0;
   }
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -1300,7 +1300,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       sstep_virtual(cur, fa, fb, c, vwt, key0, hi, w);
     }
   };
-  if constexpr (MODE == kSparse) {
+  if constexpr (MODE == kSparse || MODE == kSparseComp) {
     // Step records in registers: lane i of win_a / win_b holds sub-block a /
     // b of step 64 m + i of the current window m, as (first key row << 6 |
     // valid keys of the sub-block, clamped to 0 .. 32), decoded from the LDS
@@ -1377,8 +1377,12 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     // stalls on them.
     // kind: 0 a wave with a real query row, 1 the wave that computes the
     // all-zero groups' output, 2 a copy wave (loads only)
+    // Compensated attention: the last list step loads the first virtual
+    // step (the tile summaries) instead.
+    const bool virt_next = MODE == kSparseComp && n_virt > 0;
     auto step = [&](auto kind, bool more, uint32_t ra, uint32_t rb, const lds_u8* cur,
-                    uint32_t na, uint32_t nb, uint32_t nxt) __attribute__((always_inline)) {
+                    uint32_t na, uint32_t nb, uint32_t nxt, lds_u8* nxt_slot)
+        __attribute__((always_inline)) {
       const int la = (int)(ra & 63u), lb = (int)(rb & 63u);
       const char *kb, *vb;
       rec_base(na, nb, kb, vb);
@@ -1386,11 +1390,15 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
         if (more) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) issue(kb, vb, j, nxt);
+        } else if (virt_next) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) virtual_seg(0, nxt_slot, j);
         }
         if constexpr (decltype(kind)::value == 1) sstep_zero_q(cur, fa, fb, la, lb, hi, w);
       } else {
         sstep(cur, fa, fb, c, la, lb, hi, w, [&](int k) {
           if (more) issue(kb, vb, k, nxt);
+          else if (virt_next) virtual_seg(0, nxt_slot, k);
         });
       }
     };
@@ -1399,26 +1407,28 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     // and loads step u + 1 into the other.
     auto walk = [&](auto zero) __attribute__((always_inline)) {
       uint32_t ca = 0, cb = 0;
-      if (n_steps > 0) {
+      if (n_lsteps > 0) {
         fetch(0, ca, cb);
         const char *kb, *vb;
         rec_base(ca, cb, kb, vb);
 #pragma unroll
         for (int j = 0; j < 8; ++j) issue(kb, vb, j, lds_s0);
+      } else if (virt_next) {
+        load_virtual(0, s0);
       }
-      for (int u = 0; u < n_steps; u += 2) {
+      for (int u = 0; u < n_lsteps; u += 2) {
         uint32_t na = 0, nb = 0;
         VEDA_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
-        const bool more1 = u + 1 < n_steps;
+        const bool more1 = u + 1 < n_lsteps;
         if (more1) fetch(u + 1, na, nb);
-        step(zero, more1, ca, cb, s0, na, nb, lds_s1);
+        step(zero, more1, ca, cb, s0, na, nb, lds_s1, s1);
         if (!more1) break;
         VEDA_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
-        const bool more2 = u + 2 < n_steps;
+        const bool more2 = u + 2 < n_lsteps;
         if (more2) fetch(u + 2, ca, cb);
-        step(zero, more2, na, nb, s1, ca, cb, lds_s0);
+        step(zero, more2, na, nb, s1, ca, cb, lds_s0, s0);
       }
     };
     if (copy)
@@ -1427,6 +1437,33 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       walk(std::integral_constant<int, 1>{});
     else
       walk(std::integral_constant<int, 0>{});
+    if constexpr (MODE == kSparseComp) {
+      // a row that kept nothing: the reference's unit mass at reference 0
+      // (a select, not a branch: the condition is per row)
+      const bool empty = half_swap_sum(w.l_run) == 0.f;
+      w.m_run = empty ? 0.f : w.m_run;
+      w.l_run = empty ? (hi == 0 ? 1.f : 0.f) : w.l_run;
+      // the virtual steps: step u from slot u % 2 (the first one's loads
+      // were issued by the last list step, or above), each issuing the next
+      int u = n_lsteps;
+      if (u & 1) {
+        if (u < n_steps) {
+          begin_step(u, s0);
+          virtual_step(u, s1);
+          ++u;
+        }
+      }
+      for (; u + 1 < n_steps; u += 2) {
+        begin_step(u, s1);
+        virtual_step(u, s0);
+        begin_step(u + 1, s0);
+        virtual_step(u + 1, s1);
+      }
+      if (u < n_steps) {
+        begin_step(u, s1);
+        virtual_step(u, s0);
+      }
+    }
   } else {
   if (n_steps > 0 && MODE != kVirtualOnly) load_step(0, s0);  // kVirtualOnly: issued at set-up
   if (!VKEYS) {
