@@ -596,12 +596,6 @@ __device__ __forceinline__ f32x16 sub_scores(const lds_u8* slot, const HFrag& f,
   return s;
 }
 
-// A hook called between the fragment reads and the products of a step (the
-// sparse walk issues the next step's loads there); the default does nothing.
-struct NoHook {
-  __device__ __forceinline__ void operator()(int) const {}
-};
-
 // Scores of both 32-key sub-blocks of a step, as two interleaved MFMA
 // chains (each fragment read has the other chain's product to hide behind),
 // then the masks of sub-blocks with fewer than 32 valid keys.

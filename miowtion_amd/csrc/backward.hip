@@ -310,28 +310,52 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
   };
   auto entry = [&](int u) { return __builtin_amdgcn_readfirstlane((int)steps[u]); };
   // One 32-key half kh of a step with `lim` valid keys in it (lim >= 32: all).
-  auto half_step = [&](const lds_u8* slot, int kh, int lim) {
+  // hook(s) runs between the score products (the walk issues the next
+  // step's eight loads there); with a hook the order is written out in the
+  // program (a hook that branches ends the scheduling region).
+  auto half_step = [&](const lds_u8* slot, int kh, int lim, auto hook) {
     const lds_u8* ks = slot + kh * 32 * 256;
     const lds_u8* vs = slot + kHalfBytes + kh * 32 * 256;
     f32x16 st, dp = neg_d;
 #pragma unroll
     for (int e = 0; e < 16; ++e) st[e] = 0.f;
-    // S^T and dP^T as two interleaved chains, the reads of k-step s + 2
-    // issued before the products of s
+    if constexpr (std::is_same<decltype(hook), NoHook>::value) {
+      // S^T and dP^T as two interleaved chains, the reads of k-step s + 2
+      // issued before the products of s
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const u32x4 ka = lds16(ks + f.row[s]);
-      const u32x4 va = lds16(vs + f.row[s]);
-      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka), qf[s], st, 0, 0, 0);
-      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(va), dof[s], dp, 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      for (int s = 0; s < 8; ++s) {
+        const u32x4 ka = lds16(ks + f.row[s]);
+        const u32x4 va = lds16(vs + f.row[s]);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka), qf[s], st, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(va), dof[s], dp, 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int s = 0; s < 6; ++s) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      for (int s = 0; s < 6; ++s) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    } else {
+      // the same reads two k-steps ahead and products, in program order,
+      // hook(s) before the reads of k-step s + 2
+      u32x4 ka[8], va[8];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        ka[s] = lds16(ks + f.row[s]);
+        va[s] = lds16(vs + f.row[s]);
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        hook(s);
+        if (s + 2 < 8) {
+          ka[s + 2] = lds16(ks + f.row[s + 2]);
+          va[s + 2] = lds16(vs + f.row[s + 2]);
+        }
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka[s]), qf[s], st, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(va[s]), dof[s], dp, 0, 0, 0);
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     float ds[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -361,9 +385,9 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   };
-  auto compute = [&](int vch, const lds_u8* slot) {
-    half_step(slot, 0, vch);
-    if (vch > 32) half_step(slot, 1, vch - 32);
+  auto compute = [&](int vch, const lds_u8* slot, auto hook) {
+    half_step(slot, 0, vch, hook);
+    if (vch > 32) half_step(slot, 1, vch - 32, NoHook{});
   };
 
   lds_u8* s0 = (lds_u8*)ring[0];
@@ -381,8 +405,19 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
     VEDA_WAIT_VM(0);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");  // no LDS read of step u above the barrier
-    if (u + 1 < n_steps) load_step(tn, nxt);
-    compute(vch, cur);
+    // step u + 1's loads go out between step u's first score products (in
+    // one burst after the barrier, every wave of the CU queues at the load
+    // path at once)
+    const bool more = u + 1 < n_steps;
+    const int64_t row0 = (int64_t)(tn >> 1) * kTile + (tn & 1) * kHalf;
+    const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
+    const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
+    compute(vch, cur, [&](int s) {
+      if (more) {
+        if (s < 4) dma16(kb, koff[s], nxt + (4 * wave + s) * 1024);
+        else dma16(vb, voff[s - 4], nxt + kHalfBytes + (4 * wave + s - 4) * 1024);
+      }
+    });
   };
   if (n_steps > 0) load_step(entry(0), s0);
   for (int u = 0; u < n_steps; u += 2) {

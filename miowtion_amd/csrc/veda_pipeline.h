@@ -114,6 +114,12 @@ __device__ __forceinline__ void front_first(int64_t b, int64_t n_heads, int64_t 
   }
 }
 
+// A hook called between the fragment reads and the products of a step (the
+// walks issue the next step's loads there); the default does nothing.
+struct NoHook {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+
 // vmcnt waits as s_waitcnt immediates (gfx9 encoding: vmcnt low bits [3:0],
 // expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
 #define VEDA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
