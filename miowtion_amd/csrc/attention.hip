@@ -1460,7 +1460,47 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     }
   } else {
   if (n_steps > 0 && MODE != kVirtualOnly) load_step(0, s0);  // kVirtualOnly: issued at set-up
-  if (!VKEYS) {
+  if constexpr (DENSE) {
+    // Dense walk: step u is key rows 64 u .. of the used rows, from slot
+    // u % 2. It waits for its own loads and passes the barrier, then issues
+    // step u + 1's loads between its score products (as the sparse walk
+    // does), the last step's rows clamped to the used ones.
+    auto dstep = [&](int u, const lds_u8* cur, lds_u8* nxt) {
+      VEDA_WAIT_VM(0);
+      __builtin_amdgcn_s_barrier();
+      const bool more = u + 1 < n_steps;
+      const int64_t row0 = (int64_t)u * kHalf;
+      const int vch = (int)min(p.used - row0, (int64_t)kHalf);
+      const int64_t nrow0 = row0 + kHalf;
+      const int nvch = more ? (int)min(p.used - nrow0, (int64_t)kHalf) : 0;
+      // waves 0, 1 load sub-block a, waves 2, 3 sub-block b (rows from 32)
+      const int64_t nbase = nvch == kHalf && wave >= 2 ? nrow0 + 32 : nrow0;
+      const char* kb = reinterpret_cast<const char*>(kbase + nbase * p.ks);
+      const char* vb = reinterpret_cast<const char*>(vbase + nbase * p.vs);
+      const int lr = lane >> 4, pc = lane & 15;
+      auto hook = [&](int j) {
+        if (!more) return;
+        const int u4 = j & 3, seg = 4 * wave + u4;
+        lds_u8* dst = nxt + (j < 4 ? 0 : kHalfBytes) + seg * 1024;
+        if (nvch == kHalf) {
+          dma16(j < 4 ? kb : vb, j < 4 ? dma.k[u4] : dma.v[u4], dst);
+        } else {
+          // the last step: rows past `used` may not exist, so every lane
+          // reads a row below nvch (masked keys)
+          const int row = 4 * seg + lr, src = min(row, nvch - 1);
+          const uint32_t off = j < 4 ? (uint32_t)((src * p.ks + ((pc ^ (row & 15)) << 3)) * 2)
+                                     : (uint32_t)((src * p.vs + ((pc ^ ((row & 3) << 2)) << 3)) * 2);
+          dma16(j < 4 ? kb : vb, off, dst);
+        }
+      };
+      sstep(cur, fa, fb, c, vch, vch - 32, hi, w, hook);
+    };
+    for (int u = 0; u < n_steps; u += 2) {
+      dstep(u, s0, s1);
+      if (u + 1 >= n_steps) break;
+      dstep(u + 1, s1, s0);
+    }
+  } else if constexpr (!VKEYS) {
     for (int u = 0; u < n_steps; u += 2) {
       begin_step(u, s1);
       list_step(u, s0);
