@@ -206,6 +206,34 @@ int veda_block_sparse_fwd_seq(const void* q, int64_t q_rows, int64_t seq_heads,
                               int64_t front_tiles, void* stream);
 
 /*
+ * veda_block_sparse_fwd_seq with the gather of the key tiles fused in as
+ * well: k and v are in sequence order like q (bf16 [q_rows, seq_heads, D],
+ * the three sharing stride_s / stride_h), and key tile row t is row
+ * gather_index[t] of them; head h' of the lists reads head heads[h'] of k
+ * and v. Equal to veda_gather_tiles of q, k and v (gather_index, padding
+ * slots zero), then veda_block_sparse_fwd, then veda_scatter_tiles of the
+ * result, for every finite input: a padding row of a key tile (masked, p =
+ * 0) is read from that tile's first row instead of as zeros, so a
+ * non-finite value there reaches only the query tiles that keep the block,
+ * which that row already reaches. Replaces gather_tiles of q, k and v,
+ * fa4.block_sparse_attention and scatter_tiles_ inside the reference's
+ * SparseStudent._attend (miowtion/veda/attention.py:760-788). Lists,
+ * valid_count, scale and front_tiles as veda_block_sparse_fwd; no LSE.
+ * (q_rows - 1) * stride_s * 2 + 256 must be below 2^32.
+ */
+int veda_block_sparse_fwd_seq_kv(const void* q, const void* k, const void* v, int64_t q_rows,
+                                 int64_t seq_heads, int64_t stride_s, int64_t stride_h,
+                                 const int64_t* gather_index, const int64_t* scatter_index,
+                                 const int32_t* slot_valid, const int64_t* heads,
+                                 int64_t n_heads, int64_t head_dim, int64_t n_q_tiles,
+                                 int64_t n_k_tiles, const int32_t* full_cnt,
+                                 const int32_t* full_idx, const int32_t* part_cnt,
+                                 const int32_t* part_idx, int64_t list_ld,
+                                 const int32_t* valid_count, float scale, void* out,
+                                 int64_t out_rows, int64_t o_stride_s, int64_t o_stride_h,
+                                 int64_t front_tiles, void* stream);
+
+/*
  * Dense attention of rows [0, used) among themselves on packed [S, H, D]
  * rows (the h3 dense path, miowtion/h3/attention.py:28-102): out rows
  * [used, S) are 0 and their lse is 0. lse: fp32 or NULL, element

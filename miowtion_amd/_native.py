@@ -34,6 +34,8 @@ SIGNATURES: dict[str, list] = {
     'veda_block_sparse_fwd_seq': [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I,
                                   _I, _I, _I, _P, _P, _P, _P, _I, _P, _F, _P, _I, _I, _I, _I,
                                   _P],
+    'veda_block_sparse_fwd_seq_kv': [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I,
+                                     _I, _P, _P, _P, _P, _I, _P, _F, _P, _I, _I, _I, _I, _P],
     'veda_dense_fwd': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _F, _P,
                        _I, _I, _P, _I, _I, _P],
     'veda_block_heat': [_P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I,

@@ -121,6 +121,15 @@ class ClipTiling:
 _HEAD_DIM_BYTES = 128 * 2
 
 
+def _seq_kv_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """Whether the attention kernel can read k and v in sequence order: laid
+    out as q, and every row within a 32-bit load offset of its head's first
+    row."""
+    return (k.shape == q.shape and v.shape == q.shape and k.stride() == q.stride()
+            and v.stride() == q.stride() and k.dtype == q.dtype and v.dtype == q.dtype
+            and (q.shape[0] - 1) * q.stride(0) * 2 + 2 * q.shape[2] < 1 << 32)
+
+
 def _chunk_heads(tile_layout: tiling.TileLayout, collect_bytes: int) -> int:
     """Heads per chunk so one tile-ordered copy stays under collect_bytes."""
     return max(1, collect_bytes // (tile_layout.num_slots * _HEAD_DIM_BYTES))
@@ -198,21 +207,33 @@ class SparseStudent:
         cfg = self.clip.config
         compensated = cfg.zero_order_compensation or cfg.triton_compensation
         # Without compensation the attention kernel reads q in sequence order
-        # and scatters its rows itself, so q is only pooled, not permuted.
+        # and scatters its rows itself, so q is only pooled, not permuted;
+        # when k and v are laid out as q it gathers their key tiles itself
+        # too, so they are only pooled (k) or not touched (v) here.
         q_tiles = None
         if compensated:
             q_res = kernels.gather_and_pool(q, tile_layout, heads, second=bool(want))
             q_tiles, q_res = q_res[0], q_res[1:]
         else:
             q_res = kernels.pool_seq(q, tile_layout, heads, second=bool(want))
+        kv_seq = not compensated and _seq_kv_ok(q, k, v)
+        k_tiles = v_tiles = None
         if want:
             feats_q, sq_q, _ = q_res
-            k_tiles, feats_k, _, var_k = kernels.gather_and_pool(k, tile_layout, heads, second=True)
+            if kv_seq:
+                feats_k, _, var_k = kernels.pool_seq(k, tile_layout, heads, second=True)
+            else:
+                k_tiles, feats_k, _, var_k = kernels.gather_and_pool(k, tile_layout, heads,
+                                                                     second=True)
         else:
             (feats_q,) = q_res
-            k_tiles, feats_k = kernels.gather_and_pool(k, tile_layout, heads)
+            if kv_seq:
+                (feats_k,) = kernels.pool_seq(k, tile_layout, heads)
+            else:
+                k_tiles, feats_k = kernels.gather_and_pool(k, tile_layout, heads)
             sq_q = var_k = None
-        v_tiles = kernels.gather_tiles(v, tile_layout, heads)
+        if not kv_seq:
+            v_tiles = kernels.gather_tiles(v, tile_layout, heads)
         with torch.no_grad():
             extra = {}
             if pred.count_term:
@@ -229,6 +250,8 @@ class SparseStudent:
                 o_tiles = kernels.compensated_attention(q_tiles, k_tiles, v_tiles, block_mask,
                                                         tile_layout, lists)
                 kernels.scatter_tiles_(out, o_tiles, tile_layout, heads)
+            elif kv_seq:
+                kernels.block_sparse_attention_seq_kv_(out, q, k, v, lists, tile_layout, heads)
             else:
                 kernels.block_sparse_attention_seq_(out, q, k_tiles, v_tiles, lists, tile_layout,
                                                     heads)

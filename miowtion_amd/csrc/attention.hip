@@ -953,7 +953,11 @@ __device__ __forceinline__ void sstep_virtual(const lds_u8* slot, const HFrag& f
 // and lse 0.
 enum SparseMode { kSparse = 0, kVirtualOnly = 1, kSparseComp = 2, kDenseRows = 3 };
 
-template <int MODE>
+// SEQKV (kSparse in sequence order only): k and v are in sequence order too
+// ([seq_rows, seq_heads_n, D], as q), and key tile row t of a step is read
+// from row seq_q[t] of them (the gather of the key tiles fused into the
+// walk).
+template <int MODE, bool SEQKV = false>
 __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   constexpr bool DENSE = MODE == kDenseRows;
   constexpr bool LISTS = MODE == kSparse || MODE == kSparseComp;  // walks the block lists
@@ -1425,12 +1429,133 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
         step(zero, more2, na, nb, s1, ca, cb, lds_s0, s0);
       }
     };
-    if (copy)
-      walk(std::integral_constant<int, 2>{});
-    else if (q_zero)
-      walk(std::integral_constant<int, 1>{});
-    else
-      walk(std::integral_constant<int, 0>{});
+    // Sequence-order k / v: this wave's four segments of a step are rows
+    // 16 (wave & 1) + 4 u4 + lane / 16 of its sub-block; each is read from
+    // the row its slot gathers (the low word of the int64 gather index),
+    // and a row past the sub-block's valid keys (padding, masked) from the
+    // sub-block's first row, a real row of the same key tile (so a
+    // non-finite value there reaches only query tiles that keep the block,
+    // as in the tiled form). The rows of step u + 2 are looked up during
+    // step u, so the step's loads wait for no lookup.
+    const int32_t* tok_of = reinterpret_cast<const int32_t*>(p.seq_q);
+    const int kv_head = SEQKV ? (int)min(max(p.seq_heads[head], (int64_t)0), p.seq_heads_n - 1) : 0;
+    const char* kseq = reinterpret_cast<const char*>(p.k + (int64_t)kv_head * p.kh);
+    const char* vseq = reinterpret_cast<const char*>(p.v + (int64_t)kv_head * p.vh);
+    auto tokens = [&](uint32_t ra, uint32_t rb, int32_t (&t)[4]) {
+      const uint32_t rec = wave < 2 ? ra : rb;
+      const int64_t base = (int64_t)(rec >> 6);
+      const int lim = (int)(rec & 63u);
+#pragma unroll
+      for (int u4 = 0; u4 < 4; ++u4) {
+        const int src = 16 * (wave & 1) + 4 * u4 + (lane >> 4);
+        t[u4] = tok_of[2 * (base + (src < lim ? src : 0))];
+      }
+    };
+    // byte offset of a row: row * (2 stride_s) fits 32 bits (the launcher
+    // checks), k and v share the stride; the chunk swizzles of the slot rows
+    // are per-lane constants
+    const uint32_t row_bytes = (uint32_t)(2 * p.ks);
+    const uint32_t n_rows = (uint32_t)p.seq_rows;
+    uint32_t kswz[4], vswz[4];
+#pragma unroll
+    for (int u4 = 0; u4 < 4; ++u4) {
+      const int pc = lane & 15, row = 4 * (4 * wave + u4) + (lane >> 4);  // slot row
+      kswz[u4] = (uint32_t)((pc ^ (row & 15)) << 4);
+      vswz[u4] = (uint32_t)((pc ^ ((row & 3) << 2)) << 4);
+    }
+    auto offsets = [&](const int32_t (&t)[4], uint32_t (&ok)[4], uint32_t (&ov)[4]) {
+#pragma unroll
+      for (int u4 = 0; u4 < 4; ++u4) {
+        const uint32_t tk = (uint32_t)t[u4] < n_rows ? (uint32_t)t[u4] : 0u;
+        const uint32_t b = tk * row_bytes;
+        ok[u4] = b + kswz[u4];
+        ov[u4] = b + vswz[u4];
+      }
+    };
+    auto issue_kv = [&](const uint32_t (&ok)[4], const uint32_t (&ov)[4], int j, uint32_t lds) {
+      const int u4 = j & 3;
+      if (j < 4)
+        dma16_m0(kseq, ok[u4], lds + u4 * 1024);
+      else
+        dma16_m0(vseq, ov[u4], lds + kHalfBytes + u4 * 1024);
+    };
+    auto step_kv = [&](auto kind, bool more, uint32_t ra, uint32_t rb, const lds_u8* cur,
+                       const uint32_t (&ok)[4], const uint32_t (&ov)[4], uint32_t nxt)
+        __attribute__((always_inline)) {
+      const int la = (int)(ra & 63u), lb = (int)(rb & 63u);
+      if constexpr (decltype(kind)::value != 0) {
+        if (more) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) issue_kv(ok, ov, j, nxt);
+        }
+        if constexpr (decltype(kind)::value == 1) sstep_zero_q(cur, fa, fb, la, lb, hi, w);
+      } else {
+        sstep(cur, fa, fb, c, la, lb, hi, w, [&](int k) {
+          if (more) issue_kv(ok, ov, k, nxt);
+        });
+      }
+    };
+    // the walk above with sequence-order k / v; (ra0, rb0) and (ra1, rb1)
+    // are the records of steps u and u + 1, tk the rows of the next step
+    // whose loads are not issued yet
+    auto walk_kv = [&](auto zero) __attribute__((always_inline)) {
+      uint32_t ra0 = 0, rb0 = 0, ra1 = 0, rb1 = 0;
+      int32_t tk[4] = {0, 0, 0, 0};
+      uint32_t ok[4], ov[4];
+      if (n_lsteps > 0) {
+        fetch(0, ra0, rb0);
+        tokens(ra0, rb0, tk);
+        offsets(tk, ok, ov);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) issue_kv(ok, ov, j, lds_s0);
+      }
+      if (n_lsteps > 1) {
+        fetch(1, ra1, rb1);
+        tokens(ra1, rb1, tk);
+      }
+      for (int u = 0; u < n_lsteps; u += 2) {
+        VEDA_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        const bool more1 = u + 1 < n_lsteps;
+        uint32_t ra2 = 0, rb2 = 0;
+        if (more1) offsets(tk, ok, ov);  // step u + 1
+        if (u + 2 < n_lsteps) {
+          fetch(u + 2, ra2, rb2);
+          tokens(ra2, rb2, tk);
+        }
+        step_kv(zero, more1, ra0, rb0, s0, ok, ov, lds_s1);
+        if (!more1) break;
+        VEDA_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        const bool more2 = u + 2 < n_lsteps;
+        uint32_t ra3 = 0, rb3 = 0;
+        if (more2) offsets(tk, ok, ov);  // step u + 2
+        if (u + 3 < n_lsteps) {
+          fetch(u + 3, ra3, rb3);
+          tokens(ra3, rb3, tk);
+        }
+        step_kv(zero, more2, ra1, rb1, s1, ok, ov, lds_s0);
+        ra0 = ra2;
+        rb0 = rb2;
+        ra1 = ra3;
+        rb1 = rb3;
+      }
+    };
+    if constexpr (SEQKV) {
+      if (copy)
+        walk_kv(std::integral_constant<int, 2>{});
+      else if (q_zero)
+        walk_kv(std::integral_constant<int, 1>{});
+      else
+        walk_kv(std::integral_constant<int, 0>{});
+    } else {
+      if (copy)
+        walk(std::integral_constant<int, 2>{});
+      else if (q_zero)
+        walk(std::integral_constant<int, 1>{});
+      else
+        walk(std::integral_constant<int, 0>{});
+    }
     if constexpr (MODE == kSparseComp) {
       // a row that kept nothing: the reference's unit mass at reference 0
       // (a select, not a branch: the condition is per row)
@@ -1962,6 +2087,72 @@ extern "C" int veda_block_sparse_fwd_seq(
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   sfwd_kernel<kSparse><<<(unsigned)items, kThreads2, 0, s>>>(p);
   return check_launch("veda_block_sparse_fwd_seq");
+}
+
+extern "C" int veda_block_sparse_fwd_seq_kv(
+    const void* q, const void* k, const void* v, int64_t q_rows, int64_t seq_heads,
+    int64_t stride_s, int64_t stride_h, const int64_t* gather_index, const int64_t* scatter_index,
+    const int32_t* slot_valid, const int64_t* heads, int64_t n_heads, int64_t head_dim,
+    int64_t n_q_tiles, int64_t n_k_tiles, const int32_t* full_cnt, const int32_t* full_idx,
+    const int32_t* part_cnt, const int32_t* part_idx, int64_t list_ld, const int32_t* valid_count,
+    float scale, void* out, int64_t out_rows, int64_t o_stride_s, int64_t o_stride_h,
+    int64_t front_tiles, void* stream) {
+  VEDA_REQUIRE(head_dim == kD, "block_sparse_fwd_seq_kv: head_dim must be 128, got %lld",
+               (long long)head_dim);
+  VEDA_REQUIRE(front_tiles >= 0 && front_tiles <= n_q_tiles,
+               "block_sparse_fwd_seq_kv: front_tiles %lld outside [0, n_q_tiles]",
+               (long long)front_tiles);
+  VEDA_REQUIRE(n_heads >= 0 && n_q_tiles >= 0 && n_k_tiles >= 0 && q_rows >= 0 && out_rows >= 0 &&
+                   seq_heads >= 0,
+               "block_sparse_fwd_seq_kv: negative size");
+  VEDA_REQUIRE(list_ld >= n_k_tiles, "block_sparse_fwd_seq_kv: list_ld %lld < n_k_tiles %lld",
+               (long long)list_ld, (long long)n_k_tiles);
+  VEDA_REQUIRE(gather_index != nullptr && scatter_index != nullptr && slot_valid != nullptr &&
+                   heads != nullptr,
+               "block_sparse_fwd_seq_kv: the gather / scatter indices, slot_valid and heads are "
+               "required");
+  VEDA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) &&
+                   stride_s % 8 == 0 && stride_h % 8 == 0 && o_stride_s % 4 == 0 &&
+                   o_stride_h % 4 == 0,
+               "block_sparse_fwd_seq_kv: rows must be 16-byte aligned");
+  const int64_t items = n_heads * n_q_tiles;
+  if (items == 0) return VEDA_OK;
+  VEDA_REQUIRE(n_k_tiles >= 1 && n_k_tiles <= kMaxBlocks,
+               "block_sparse_fwd_seq_kv: n_k_tiles %lld outside [1, %d]", (long long)n_k_tiles,
+               kMaxBlocks);
+  VEDA_REQUIRE(q_rows >= 1 && seq_heads >= 1, "block_sparse_fwd_seq_kv: k and v need rows and heads");
+  // a key row's byte offset from its head's first row is a 32-bit load offset
+  VEDA_REQUIRE(q_rows < ((int64_t)1 << 31) && (q_rows - 1) * stride_s * 2 + 2 * kD < (int64_t)1 << 32,
+               "block_sparse_fwd_seq_kv: %lld rows of stride %lld exceed the 4 GiB load offset",
+               (long long)q_rows, (long long)stride_s);
+  FwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.qs = stride_s; p.qh = stride_h;
+  p.ks = stride_s; p.kh = stride_h;
+  p.vs = stride_s; p.vh = stride_h;
+  p.n_heads = n_heads; p.n_q_tiles = n_q_tiles; p.n_k_tiles = n_k_tiles;
+  p.full_cnt = full_cnt; p.full_idx = full_idx;
+  p.part_cnt = part_cnt; p.part_idx = part_idx;
+  p.list_ld = list_ld;
+  p.valid_count = valid_count;
+  p.q_rows = n_q_tiles * kTile;
+  p.scale_log2 = (float)((double)scale * 1.4426950408889634);
+  p.out = static_cast<uint16_t*>(out);
+  p.os = o_stride_s; p.oh = o_stride_h;
+  p.lse = nullptr;
+  p.front = front_tiles;
+  p.seq_q = gather_index;
+  p.seq_o = scatter_index;
+  p.slot_ok = slot_valid;
+  p.seq_heads = heads;
+  p.seq_rows = q_rows;
+  p.seq_heads_n = seq_heads;
+  p.out_rows = out_rows;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  sfwd_kernel<kSparse, true><<<(unsigned)items, kThreads2, 0, s>>>(p);
+  return check_launch("veda_block_sparse_fwd_seq_kv");
 }
 
 extern "C" int veda_compensated_attention(

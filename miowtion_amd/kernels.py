@@ -247,6 +247,20 @@ def block_sparse_attention_seq_(out: torch.Tensor, q: torch.Tensor, k: torch.Ten
                               _front_tiles(layout, layout.gather_index.numel() // 128))
 
 
+def block_sparse_attention_seq_kv_(out: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
+                                   v: torch.Tensor, lists, layout: tiling.TileLayout,
+                                   heads: torch.Tensor | None) -> None:
+    """block_sparse_attention_seq_ with the gather of k and v fused in too:
+    q, k, v [S, H, D] in sequence order (the sequence gather_tiles of q, k,
+    v, fa4.block_sparse_attention, scatter_tiles_ of
+    miowtion/veda/attention.py:760-788, in one kernel)."""
+    part_cnt, part_idx, full_cnt, full_idx = lists
+    ops.block_sparse_fwd_seq_kv_(out, q, k, v, layout.gather_index, layout.scatter_index,
+                                 layout.slot_valid, _heads(q, heads), part_cnt, part_idx,
+                                 full_cnt, full_idx, layout.valid_count,
+                                 _front_tiles(layout, layout.gather_index.numel() // 128))
+
+
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, used: int,
                     return_lse: bool = False):
     """Dense attention of rows [0, used) among themselves (h3/attention.py:28-102):

@@ -307,6 +307,51 @@ def block_sparse_fwd_seq_(out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v
                  out.stride(1), front_tiles, _stream(q))
 
 
+@torch.library.custom_op('veda::block_sparse_fwd_seq_kv_', mutates_args=('out',))
+def block_sparse_fwd_seq_kv_(out: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
+                             v: torch.Tensor, gather_index: torch.Tensor,
+                             scatter_index: torch.Tensor, slot_valid: torch.Tensor,
+                             heads: torch.Tensor, part_cnt: torch.Tensor, part_idx: torch.Tensor,
+                             full_cnt: torch.Tensor, full_idx: torch.Tensor,
+                             valid_count: torch.Tensor, front_tiles: int = 0) -> None:
+    """block_sparse_fwd_seq_ with k and v in sequence order too: q, k, v
+    [S, H, D] alike are read through gather_index (key tile row t is row
+    gather_index[t]), out [S + 1, H, D] receives the rows through
+    scatter_index. heads maps the H' heads of the lists to heads of q, k, v
+    and out."""
+    _require_gpu(out, q, k, v, gather_index, scatter_index, slot_valid, heads, part_cnt,
+                 part_idx, full_cnt, full_idx, valid_count)
+    for name, t in (('out', out), ('q', q), ('k', k), ('v', v)):
+        _check_rows(name, t)
+    if q.shape[-1] != 128 or out.shape[1:] != q.shape[1:] or out.dtype != q.dtype:
+        raise ValueError(f'q {tuple(q.shape)} and out {tuple(out.shape)} must be [*, H, 128] alike')
+    if k.shape != q.shape or v.shape != q.shape or k.stride() != q.stride() or v.stride() != q.stride():
+        raise ValueError(f'k {tuple(k.shape)} / v {tuple(v.shape)} must be laid out as q '
+                         f'{tuple(q.shape)}')
+    n_slots = gather_index.numel()
+    hp = heads.numel()
+    if (n_slots % TILE or scatter_index.numel() != n_slots or slot_valid.numel() != n_slots
+            or gather_index.dtype != torch.int64 or scatter_index.dtype != torch.int64
+            or slot_valid.dtype != torch.int32 or heads.dtype != torch.int64):
+        raise ValueError('gather_index / scatter_index int64 and slot_valid int32 of n_tiles * 128 '
+                         'slots, heads int64')
+    r_tiles = n_slots // TILE
+    n_k = r_tiles
+    _check_lists('part', part_cnt, part_idx, hp, r_tiles, n_k)
+    _check_lists('full', full_cnt, full_idx, hp, r_tiles, n_k)
+    if part_idx.shape[3] != full_idx.shape[3]:
+        raise ValueError('part and full lists must have the same row length')
+    if valid_count.numel() < n_k or valid_count.dtype != torch.int32:
+        raise ValueError('valid_count must be int32 [n_k_tiles]')
+    _native.call('veda_block_sparse_fwd_seq_kv', q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                 q.shape[0], q.shape[1], q.stride(0), q.stride(1), gather_index.data_ptr(),
+                 scatter_index.data_ptr(), slot_valid.data_ptr(), heads.data_ptr(), hp,
+                 q.shape[2], r_tiles, n_k, full_cnt.data_ptr(), full_idx.data_ptr(),
+                 part_cnt.data_ptr(), part_idx.data_ptr(), part_idx.shape[3],
+                 valid_count.data_ptr(), 1.0 / math.sqrt(q.shape[2]), out.data_ptr(),
+                 out.shape[0], out.stride(0), out.stride(1), front_tiles, _stream(q))
+
+
 def _check_lists(name: str, cnt: torch.Tensor, idx: torch.Tensor, heads: int, rows: int,
                  cols: int) -> None:
     if (idx.dtype != torch.int32 or idx.dim() != 4 or tuple(idx.shape[:3]) != (1, heads, rows)

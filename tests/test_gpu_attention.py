@@ -287,3 +287,69 @@ def test_sequence_order_entry_equals_gather_attend_scatter(name):
     torch.cuda.synchronize()
     assert torch.equal(got.cpu(), want.cpu())
     assert torch.equal(got[:, [0, 2]].cpu(), init[:, [0, 2]].cpu())
+
+
+@pytest.mark.parametrize('name', ['small', 'C3b', 'C2'])
+def test_sequence_order_kv_entry_equals_gather_attend_scatter(name):
+    """veda_block_sparse_fwd_seq_kv (q, k and v read through the gather
+    index, rows written through the scatter index) against gather of q, k,
+    v -> sparse forward -> scatter on the same inputs: bit-identical buffers
+    (finite inputs), padding rows and the heads outside the subset untouched.
+    The subset is heads 1 and 3 of 4; the masks keep 20 % of the blocks plus
+    the diagonal, so steps pair ragged halves of partial key tiles."""
+    spec = helpers.small_layout() if name == 'small' else helpers.CONFIGS[name]
+    lay = helpers.product_layout(*spec, device='cuda')
+    q, k, v = (t.cuda() for t in helpers.qkv(lay.seq_len, 4, 128, seed=7))
+    heads = torch.tensor([1, 3], device='cuda')
+    kt, vt = (kernels.gather_tiles(t, lay, heads) for t in (k, v))
+    g = torch.Generator().manual_seed(8)
+    mask = (torch.rand(2, lay.n_tiles, lay.n_tiles, generator=g) < 0.2) | torch.eye(
+        lay.n_tiles, dtype=torch.bool)[None]
+    lists = kernels.index_lists(mask.cuda(), lay)
+    init = torch.randn(lay.seq_len + 1, 4, 128, generator=g).to(torch.bfloat16).cuda()
+    want = init.clone()
+    kernels.block_sparse_attention_seq_(want, q, kt, vt, lists, lay, heads)
+    got = init.clone()
+    kernels.block_sparse_attention_seq_kv_(got, q, k, v, lists, lay, heads)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16).cpu(), want.view(torch.int16).cpu())
+    assert torch.equal(got[:, [0, 2]].cpu(), init[:, [0, 2]].cpu())
+    # k and v must be laid out as q
+    with pytest.raises(ValueError, match='laid out as q'):
+        kernels.block_sparse_attention_seq_kv_(got, q, k[:-1], v, lists, lay, heads)
+
+
+def test_sequence_order_kv_non_finite_rows_stay_in_their_blocks():
+    """With k / v read in sequence order a key tile's padding rows come from
+    its first real row, so an Inf in that row's v reaches exactly the query
+    tiles that keep the block (as in the tiled form, where the real row
+    itself carries it); every other row matches the tiled form bit for bit."""
+    spec = helpers.small_layout()
+    lay = helpers.product_layout(*spec, device='cuda')
+    q, k, v = (t.cuda() for t in helpers.qkv(lay.seq_len, 2, 128, seed=9))
+    heads = torch.tensor([0, 1], device='cuda')
+    vc = lay.valid_count.cpu()
+    j = int(torch.nonzero((vc > 0) & (vc < 128))[0])   # a partial key tile
+    first = int(lay.gather_index[j * 128])             # its first real row
+    v[first, :, 5] = float('inf')
+    g = torch.Generator().manual_seed(10)
+    mask = (torch.rand(2, lay.n_tiles, lay.n_tiles, generator=g) < 0.3) | torch.eye(
+        lay.n_tiles, dtype=torch.bool)[None]
+    lists = kernels.index_lists(mask.cuda(), lay)
+    kt, vt = (kernels.gather_tiles(t, lay, heads) for t in (k, v))
+    want = torch.zeros(lay.seq_len + 1, 2, 128, dtype=torch.bfloat16, device='cuda')
+    kernels.block_sparse_attention_seq_(want, q, kt, vt, lists, lay, heads)
+    got = torch.zeros_like(want)
+    kernels.block_sparse_attention_seq_kv_(got, q, k, v, lists, lay, heads)
+    torch.cuda.synchronize()
+    keeps = (mask & lay.kv_ok.cpu()[None, None, :])[:, :, j]      # [heads, query tiles]
+    rows_keep = torch.zeros(lay.seq_len + 1, 2, dtype=torch.bool)
+    sc = lay.scatter_index.cpu().view(-1, 128)
+    for h in range(2):
+        for r in torch.nonzero(keeps[h]).flatten().tolist():
+            rows_keep[sc[r], h] = True
+    gotc, wantc = got.cpu(), want.cpu()
+    bad = ~torch.isfinite(gotc.float()).all(-1)
+    assert not (bad & ~rows_keep).any()          # nothing outside the keeping tiles
+    same = ~rows_keep
+    assert torch.equal(gotc.view(torch.int16)[same], wantc.view(torch.int16)[same])
