@@ -539,6 +539,10 @@ __global__ void __launch_bounds__(kThreads) hfwd_kernel(FwdParams p) {
 
 constexpr int kThreads2 = 256;
 constexpr uint16_t kVoidStep = 0xFFFF;  // list entry outside [0, n_k): no valid key
+constexpr uint16_t kPairStep = 0x8000;  // step entry flag: a pair of ragged halves
+// Workgroups of the sparse walk resident at once on MI355X (256 CUs, two
+// each): the period of the walks' rotation over the key tiles.
+constexpr int kSweepWorkgroups = 512;
 
 // Per-lane byte offsets of this wave's eight 1 KB segments of a step
 // (segments 4 w + u, u = 0..3, of K and of V: rows 4 seg + l / 16), and of
@@ -967,7 +971,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   __shared__ uint8_t tvc[LISTS ? kMaxBlocks : 1];
   // virtual keys: per key tile, its real row count if dropped, else 0
   __shared__ __attribute__((aligned(16))) uint8_t vwt[VKEYS ? kMaxBlocks + kHalf : 4];
-  __shared__ int32_t step_total, step_big, step_small;
+  __shared__ int32_t step_total, step_small, list_bad, list_unsorted;
   // sparse walk: which waves' 32 query rows are all zero, and the LSE of
   // their rows (all alike; see the copy waves below)
   __shared__ uint8_t zflag[4];
@@ -1060,13 +1064,27 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     if (tid == 0) step_total = DENSE ? (int)((p.used + kHalf - 1) / kHalf) : 0;
   } else {
     // Step list of 64-key halves (j << 2 | half << 1 | full), valid counts
-    // in a byte table. Halves with more than 32 valid keys take a step each,
-    // from the front of `steps`: the full-list tiles' two halves, then the
-    // partial-list halves in list order. Halves with 1..32 valid keys (the
-    // ragged ends of partial tiles) go to the back of `steps`, downwards,
-    // and are computed two to a step (one per 32-key sub-block), so no
-    // step leaves a sub-block idle. Ranks come from ballots, so the order,
-    // and with it the summation order, is deterministic.
+    // in a byte table. A half with more than 32 valid keys (or a tile with
+    // none: one void step) takes a step. Halves with 1..32 valid keys (the
+    // ragged ends of partial tiles) are computed two to a step, one per
+    // 32-key sub-block, so no step leaves a sub-block idle: the first of a
+    // pair takes the step at its own place, flagged kPairStep, and the second
+    // (its partner) is stored from the back of `steps` downwards, by pair
+    // index.
+    //
+    // Walk order: the key tiles of both lists merged in ascending order,
+    // starting at the first kept tile at or past tile r n_k / 512 (mod n_k)
+    // and wrapping. The ~512 workgroups resident at once are consecutive
+    // query tiles of a head, each started about 1/512 of a walk after the
+    // previous one, so with this rotation they sweep the head's key tiles
+    // together: a K/V line one of them fetches past L2 is more often still
+    // there when the next workgroup of its XCD that keeps the tile reads it.
+    // The rotation depends on the query tile alone, so the order (and the
+    // summation order with it) is the same whichever heads a launch holds.
+    // Lists that are not strictly ascending, share a tile, or hold an entry
+    // outside [0, n_k) keep list order instead (the full list, then the
+    // partial list, every entry as listed; an entry outside [0, n_k) is
+    // void: two steps in the full list, one in the partial list).
     const int64_t li_ = head * p.n_q_tiles + r;
     const int ld = (int)p.list_ld;
     const int32_t* fl = p.full_idx + li_ * p.list_ld;
@@ -1078,49 +1096,150 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     const int nf = min(max(p.full_cnt[li_], 0), min(ld, kMaxBlocks));
     const int np = min(max(p.part_cnt[li_], 0), min(ld, kMaxBlocks - nf));
     for (int j = tid; j < nk; j += kThreads2) tvc[j] = (uint8_t)min(max(p.valid_count[j], 0), kTile);
-    __syncthreads();  // valid counts in LDS
+    // scratch in ring slot 1 (12 KB), which no load targets before the
+    // walk's first barrier: both lists, then the walk order (j << 1 | full)
+    uint16_t* sf = reinterpret_cast<uint16_t*>(&ring[1][0]);
+    uint16_t* sp = sf + kMaxBlocks;
+    uint16_t* sm = sp + kMaxBlocks;
+    constexpr uint16_t kBadFull = 0xFFFF, kBadPart = 0xFFFE;  // entries outside [0, n_k)
+    if (tid == 0) {
+      list_bad = 0;
+      list_unsorted = 0;
+    }
+    __syncthreads();  // valid counts in LDS, flags cleared
+    bool bad = false;
     for (int i = tid; i < nf; i += kThreads2) {
       const int32_t j = i < kThreads2 ? f0 : fl[i];
       const bool ok = j >= 0 && j < nk;
-      steps[2 * i] = ok ? (uint16_t)((j << 2) | 1) : kVoidStep;
-      steps[2 * i + 1] = ok ? (uint16_t)((j << 2) | 3) : kVoidStep;
+      bad |= !ok;
+      sf[i] = ok ? (uint16_t)j : kBadFull;
+    }
+    for (int i = tid; i < np; i += kThreads2) {
+      const int32_t j = i < kThreads2 ? p0 : pl[i];
+      const bool ok = j >= 0 && j < nk;
+      bad |= !ok;
+      sp[i] = ok ? (uint16_t)j : kBadPart;
+    }
+    if (bad) list_bad = 1;
+    __syncthreads();  // both lists in LDS
+    // entries of a[0, n) below `key` (a ascending)
+    auto below = [](const uint16_t* a, int n, int key) {
+      int lo = 0, up = n;
+      while (lo < up) {
+        const int mid = (lo + up) >> 1;
+        if ((int)a[mid] < key)
+          lo = mid + 1;
+        else
+          up = mid;
+      }
+      return lo;
+    };
+    if (__builtin_amdgcn_readfirstlane(list_bad) == 0) {
+      // an entry's place in the merged order: its index plus the entries of
+      // the other list with a lower tile
+      bool uns = false;
+      for (int i = tid; i < nf; i += kThreads2) {
+        const int j = sf[i];
+        const int k = below(sp, np, j);
+        uns |= (i > 0 && sf[i - 1] >= j) || (k < np && sp[k] == j);
+        sm[i + k] = (uint16_t)((j << 1) | 1);
+      }
+      for (int i = tid; i < np; i += kThreads2) {
+        const int j = sp[i];
+        const int k = below(sf, nf, j);
+        uns |= (i > 0 && sp[i - 1] >= j) || (k < nf && sf[k] == j);
+        sm[i + k] = (uint16_t)(j << 1);
+      }
+      if (uns) list_unsorted = 1;
+    }
+    __syncthreads();  // merged order (if the lists allow it)
+    const bool sweep = __builtin_amdgcn_readfirstlane(list_bad | list_unsorted) == 0;
+    if (!sweep) {
+      for (int i = tid; i < nf; i += kThreads2)
+        sm[i] = sf[i] == kBadFull ? kBadFull : (uint16_t)((sf[i] << 1) | 1);
+      for (int i = tid; i < np; i += kThreads2)
+        sm[nf + i] = sp[i] == kBadPart ? kBadPart : (uint16_t)(sp[i] << 1);
+      __syncthreads();  // list order
     }
     if (wave == 0) {
-      int na = 2 * nf, nb = 0;
-      for (int i0 = 0; i0 < np; i0 += 64) {
-        const int i = i0 + lane;
-        int vc = 0;
-        int32_t j = -1;
-        bool ok = false;
-        if (i < np) {
-          j = i0 == 0 ? p0 : pl[i];
-          ok = j >= 0 && j < nk;
-          if (ok) vc = tvc[j];
+      const int nm = nf + np;
+      int m0 = 0;  // the walk's first entry
+      if (sweep && nm > 0) {
+        const int start = (int)((r * (int64_t)nk / kSweepWorkgroups) % nk);
+        int lo = 0, up = nm;
+        while (lo < up) {
+          const int mid = (lo + up) >> 1;
+          if ((int)(sm[mid] >> 1) < start)
+            lo = mid + 1;
+          else
+            up = mid;
         }
-        // an entry outside [0, n_k) or a tile with no valid key: one void
-        // step, as a full-list entry outside [0, n_k) is
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int vch = half ? vc - kHalf : min(vc, kHalf);
-          const bool has = i < np && (half == 0 || vch > 0);
-          const bool big = has && (vch > 32 || vc == 0);
-          const bool small = has && !big;
-          const uint16_t e = ok && vc > 0 ? (uint16_t)((j << 2) | (half << 1)) : kVoidStep;
-          const uint64_t ba = __ballot(big), bs = __ballot(small);
-          const int ra = __builtin_amdgcn_mbcnt_hi((uint32_t)(ba >> 32),
-                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)ba, 0));
-          const int rs = __builtin_amdgcn_mbcnt_hi((uint32_t)(bs >> 32),
-                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bs, 0));
-          if (big) steps[na + ra] = e;
-          if (small) steps[2 * kMaxBlocks - 1 - (nb + rs)] = e;
-          na += __builtin_popcountll(ba);
-          nb += __builtin_popcountll(bs);
+        m0 = lo == nm ? 0 : lo;
+      }
+      // one entry per lane: its halves' steps at their places, from the
+      // counts of big and ragged halves before them (ballots, so the order is
+      // deterministic)
+      int nbig = 0, nsm = 0;
+      for (int q0 = 0; q0 < nm; q0 += 64) {
+        const int q = q0 + lane;
+        int m = q + m0;
+        if (m >= nm) m -= nm;
+        uint16_t e0 = kVoidStep, e1 = kVoidStep;
+        bool b0 = false, r0 = false, b1 = false, r1 = false;  // big / ragged half 0, 1
+        if (q < nm) {
+          const uint16_t code = sm[m];
+          if (code == kBadFull) {
+            b0 = b1 = true;
+          } else if (code == kBadPart) {
+            b0 = true;
+          } else {
+            const int j = code >> 1;
+            if (code & 1) {
+              e0 = (uint16_t)((j << 2) | 1);
+              e1 = (uint16_t)((j << 2) | 3);
+              b0 = b1 = true;
+            } else {
+              const int vc = tvc[j];
+              if (vc == 0) {
+                b0 = true;  // no valid key: one void step
+              } else {
+                e0 = (uint16_t)(j << 2);
+                b0 = min(vc, kHalf) > 32;
+                r0 = !b0;
+                if (vc > kHalf) {
+                  e1 = (uint16_t)((j << 2) | 2);
+                  b1 = vc - kHalf > 32;
+                  r1 = !b1;
+                }
+              }
+            }
+          }
         }
+        const int cb = (int)b0 + (int)b1, cr = (int)r0 + (int)r1;
+        const uint64_t bb1 = __ballot(cb & 1), bb2 = __ballot(cb >> 1);
+        const uint64_t br1 = __ballot(cr & 1), br2 = __ballot(cr >> 1);
+        auto below_lane = [&](uint64_t b) {
+          return __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0));
+        };
+        const int B = nbig + below_lane(bb1) + 2 * below_lane(bb2);
+        const int S = nsm + below_lane(br1) + 2 * below_lane(br2);
+        // a big half's step follows the big halves and the pairs begun before it
+        auto put = [&](uint16_t e, bool big, int bx, int sx) {
+          if (big)
+            steps[bx + ((sx + 1) >> 1)] = e;
+          else if ((sx & 1) == 0)
+            steps[bx + (sx >> 1)] = (uint16_t)(e | kPairStep);
+          else
+            steps[2 * kMaxBlocks - 1 - (sx >> 1)] = e;
+        };
+        if (b0 || r0) put(e0, b0, B, S);
+        if (b1 || r1) put(e1, b1, B + (int)b0, S + (int)r0);
+        nbig += __builtin_popcountll(bb1) + 2 * __builtin_popcountll(bb2);
+        nsm += __builtin_popcountll(br1) + 2 * __builtin_popcountll(br2);
       }
       if (lane == 0) {
-        step_total = na + (nb + 1) / 2;
-        step_big = na;
-        step_small = nb;
+        step_total = nbig + (nsm + 1) / 2;
+        step_small = nsm;
       }
     }
   }
@@ -1166,26 +1285,13 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     has_copy = __builtin_popcount(zbits) >= 2;
   }
   const int n_lsteps = __builtin_amdgcn_readfirstlane(step_total);
-  const int n_big = LISTS ? __builtin_amdgcn_readfirstlane(step_big) : 0;
   const int n_small = LISTS ? __builtin_amdgcn_readfirstlane(step_small) : 0;
   const int n_steps = n_lsteps + n_virt;
 
-  // (first key row, valid keys) of a list half
-  auto half_keys = [&](int e, int64_t& row0, int& vch) {
-    if (e == kVoidStep) {
-      row0 = 0;
-      vch = 0;
-      return;
-    }
-    const int j = e >> 2, half = (e >> 1) & 1, full = e & 1;
-    const int vc = full ? kTile : __builtin_amdgcn_readfirstlane(tvc[j]);
-    row0 = (int64_t)j * kTile + half * kHalf;
-    vch = half ? vc - kHalf : min(vc, kHalf);
-  };
-  // Step u: sub-block a is key rows row0 .. + 31 with la valid keys,
-  // sub-block b rows rowb .. + 31 with lb (as sub_scores' lim). A 64-key
-  // step has rowb = row0 + 32, lb = la - 32; a step of two ragged halves
-  // takes one each. Steps n_lsteps .. are virtual.
+  // Step u of the virtual and dense walks (the list walk decodes its own
+  // steps): sub-block a is key rows row0 .. + 31 with la valid keys, sub-block
+  // b rows rowb .. + 31 with lb (as sub_scores' lim). Steps n_lsteps .. are
+  // virtual.
   auto decode = [&](int u, int64_t& row0, int& la, int64_t& rowb, int& lb) {
     if (VKEYS && u >= n_lsteps) {
       const int v = u - n_lsteps;
@@ -1194,18 +1300,9 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     } else if (DENSE) {
       row0 = (int64_t)u * kHalf;
       la = (int)min(p.used - row0, (int64_t)kHalf);
-    } else if (u < n_big) {
-      half_keys(__builtin_amdgcn_readfirstlane(steps[u]), row0, la);
     } else {
-      const int k = 2 * (u - n_big);
-      half_keys(__builtin_amdgcn_readfirstlane(steps[2 * kMaxBlocks - 1 - k]), row0, la);
-      if (k + 1 < n_small) {
-        half_keys(__builtin_amdgcn_readfirstlane(steps[2 * kMaxBlocks - 2 - k]), rowb, lb);
-      } else {
-        rowb = 0;
-        lb = 0;
-      }
-      return;
+      row0 = 0;
+      la = 0;
     }
     rowb = row0 + 32;
     lb = la - 32;
@@ -1283,12 +1380,6 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     else if (kept_lds)
       load_kept(nxt);
   };
-  auto list_step = [&](int u, const lds_u8* cur) {
-    int64_t row0, rowb;
-    int la, lb;
-    decode(u, row0, la, rowb, lb);
-    sstep<MODE != kDenseRows>(cur, fa, fb, c, la, lb, hi, w);
-  };
   auto virtual_step = [&](int u, const lds_u8* cur) {
     // keys past n_k carry weight 0 (the table is padded), so no mask
     const int key0 = (u - n_lsteps) * kHalf;
@@ -1307,6 +1398,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     // are issued, and carried to its compute, so the loop itself reads no
     // step list and waits on no LDS read for it.
     uint32_t win_a = 0, win_b = 0;
+    int pair_base = 0;  // pairs of ragged halves in the steps before the window
     auto lane_half = [&](int e, int64_t& r0, int& vch) {
       if (e == kVoidStep) {
         r0 = 0;
@@ -1318,21 +1410,29 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       r0 = (int64_t)j * kTile + half * kHalf;
       vch = half ? vc - kHalf : min(vc, kHalf);
     };
+    // (windows are refilled in step order, so pair_base counts the pairs
+    // before each window)
     auto refill = [&](int base) {
       const int u = base + lane;
+      const bool in = u < n_lsteps;
+      const int e = in ? (int)steps[u] : (int)kVoidStep;
+      const bool pair = in && e != kVoidStep && (e & kPairStep) != 0;
+      const uint64_t bp = __ballot(pair);
+      const int k = pair_base + __builtin_amdgcn_mbcnt_hi(
+                                    (uint32_t)(bp >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bp, 0));
+      pair_base += __builtin_popcountll(bp);
       int64_t row0 = 0, rowb = 0;
       int la = 0, lb = 0;
-      if (u < n_big) {
-        lane_half(steps[u], row0, la);
-        rowb = row0 + 32;
-        lb = la - 32;
-      } else if (u < n_lsteps) {
-        const int k = 2 * (u - n_big);
-        lane_half(steps[2 * kMaxBlocks - 1 - k], row0, la);
+      if (pair) {
+        lane_half(e & ~(int)kPairStep, row0, la);
         // the last ragged half of an odd count has no partner: sub-block b
         // loads sub-block a's rows (a kept tile), all of them masked
         rowb = row0;
-        if (k + 1 < n_small) lane_half(steps[2 * kMaxBlocks - 2 - k], rowb, lb);
+        if (2 * k + 1 < n_small) lane_half(steps[2 * kMaxBlocks - 1 - k], rowb, lb);
+      } else if (in) {
+        lane_half(e, row0, la);
+        rowb = row0 + 32;
+        lb = la - 32;
       }
       win_a = ((uint32_t)row0 << 6) | (uint32_t)min(max(la, 0), 32);
       win_b = ((uint32_t)rowb << 6) | (uint32_t)min(max(lb, 0), 32);
@@ -1625,44 +1725,11 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       if (u + 1 >= n_steps) break;
       dstep(u + 1, s1, s0);
     }
-  } else if constexpr (!VKEYS) {
-    for (int u = 0; u < n_steps; u += 2) {
-      begin_step(u, s1);
-      list_step(u, s0);
-      if (u + 1 >= n_steps) break;
-      begin_step(u + 1, s0);
-      list_step(u + 1, s1);
-    }
   } else {
-    // the list steps, then the virtual steps, as two loops (each with its
-    // own register peak); step u is in slot u % 2. Both loops are unrolled
-    // by two so that every fragment read has a constant slot address.
+    // compensation of a given output: the virtual steps, step u in slot
+    // u % 2 (step 0's loads went out at set-up), unrolled by two so that
+    // every fragment read has a constant slot address
     int u = 0;
-    for (; u + 1 < n_lsteps; u += 2) {
-      begin_step(u, s1);
-      list_step(u, s0);
-      begin_step(u + 1, s0);
-      list_step(u + 1, s1);
-    }
-    if (u < n_lsteps) {
-      begin_step(u, s1);
-      list_step(u, s0);
-      ++u;
-    }
-    if (MODE == kSparseComp) {
-      // a row that kept nothing: the reference's unit mass at reference 0
-      // (a select, not a branch: the condition is per row)
-      const bool empty = half_swap_sum(w.l_run) == 0.f;
-      w.m_run = empty ? 0.f : w.m_run;
-      w.l_run = empty ? (hi == 0 ? 1.f : 0.f) : w.l_run;
-    }
-    if (u & 1) {  // odd number of list steps: one virtual step from slot 1
-      if (u < n_steps) {
-        begin_step(u, s0);
-        virtual_step(u, s1);
-        ++u;
-      }
-    }
     for (; u + 1 < n_steps; u += 2) {
       begin_step(u, s1);
       virtual_step(u, s0);
@@ -1674,7 +1741,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       virtual_step(u, s0);
     }
   }
-  }  // MODE != kSparse
+  }  // the dense walk and the compensation of a given output
 
   const float l = half_swap_sum(w.l_run);
   // compensation: the kept output is num / den over the kept keys with

@@ -228,6 +228,54 @@ def test_front_tiles_change_the_order_only():
     assert all(torch.equal(x, y) for x, y in zip(ga, gb))
 
 
+def test_irregular_lists_keep_list_order():
+    """The walk visits a row's kept tiles in ascending key order from a
+    rotation point. Lists that are not strictly ascending or hold an entry
+    outside [0, n_k) keep list order (the full list, then the partial list)
+    and give the oracle's result as well; an entry outside [0, n_k) is a void
+    step and changes no bit of the list-order result."""
+    from miowtion_amd import ops
+    lay, olay, qt, kt, vt, mask = _case(helpers.small_layout())
+    assert olay.partial_tiles.numel() > 0 and olay.partial_tiles.numel() < lay.n_tiles
+    q, k, v, m = qt.cuda(), kt.cuda(), vt.cuda(), mask.cuda()
+    pc, pi, fc, fi = kernels.index_lists(m, lay)
+
+    def reversed_members(cnt, idx):
+        t = torch.arange(idx.shape[-1], device=idx.device)
+        c = cnt[..., None].long()
+        return idx.gather(-1, torch.where(t < c, c - 1 - t, t)).contiguous()
+
+    def with_bad_entry(cnt, idx):
+        # one more entry, past n_k, at position cnt (a row's full list holds
+        # at most the full tiles and its partial list the partial ones, so
+        # every row has room when both kinds exist)
+        assert (cnt < idx.shape[-1]).all()
+        idx = idx.clone()
+        idx.scatter_(-1, cnt.long()[..., None],
+                     torch.full_like(idx[..., :1], lay.n_tiles + 7))
+        return cnt + 1, idx
+
+    pir, fir = reversed_members(pc, pi), reversed_members(fc, fi)
+    assert not torch.equal(pir, pi) and not torch.equal(fir, fi)
+    ref, ref_lse = oa.block_sparse_attention(qt, kt, vt, mask, olay.valid_count, return_lse=True)
+    real = olay.slot_valid.bool()
+    # every row in list order: members reversed, and a void full-list entry
+    fc2, fi2 = with_bad_entry(fc, fir)
+    a = ops.block_sparse_fwd(q, k, v, pc, pir, fc2, fi2, lay.valid_count, True, 0)
+    _close(a[0], ref, real)
+    _close(a[1].T, ref_lse.T, real)
+    # a void partial-list entry too: the same bits
+    pc2, pi2 = with_bad_entry(pc, pir)
+    b = ops.block_sparse_fwd(q, k, v, pc2, pi2, fc2, fi2, lay.valid_count, True, 0)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    # ascending members with the void entries: list order with the same
+    # members, so the oracle's result again
+    c = ops.block_sparse_fwd(q, k, v, *with_bad_entry(pc, pi), *with_bad_entry(fc, fi),
+                             lay.valid_count, True, 0)
+    _close(c[0], ref, real)
+    _close(c[1].T, ref_lse.T, real)
+
+
 def test_largest_tile_count():
     """2048 tiles a side (FA4's cap on blocks per side, fa4_sm8x/block_sparsity.py:58-79;
     the kernels' list and step tables are sized to it), partial tiles
