@@ -318,8 +318,8 @@ def suite(reps: int = 5) -> dict:
     student3 = pa.SparseStudent(clip3, plan3, pred3)
     ms = _median_ms(lambda: student3(q3, k3, v3, 0), 3)
     res['veda_layer_c3'] = {'ms': round(ms, 4), 'groups': [int((choice == i).sum()) for i in (0, 1)],
-                            'bound': 'whole layer (gather/pool, predictor, selection, lists, '
-                                     'sparse forward, scatter), reported as time'}
+                            'bound': 'whole layer (pooling, predictor, selection, lists, '
+                                     'sparse forward in sequence order), reported as time'}
     del q3, k3, v3, student3, clip3
     torch.cuda.empty_cache()
 
