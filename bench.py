@@ -574,9 +574,10 @@ def main() -> int:
         'ms_per_layer': {'kernel': round(k_ms, 4), 'plus_prep': round(k_ms + prep_ms, 4),
                          'prep': round(prep_ms, 4), 'full_veda_layer': round(layer_ms, 4),
                          'full_veda_layer_predictor_lists': round(layer_pred_ms, 4),
-                         'note': 'full_veda_layer: pooling, gathers, predictor, selection, '
-                                 'lists, sparse forward with the q permutation and scatter '
-                                 'fused in, on the timed C2 patterns; '
+                         'note': 'full_veda_layer: pooling of q and k, predictor, '
+                                 'selection, lists, sparse forward reading q, k and v in '
+                                 'sequence order with the scatter fused in, on the timed C2 '
+                                 'patterns; '
                                  'full_veda_layer_predictor_lists: the same layer on the lists '
                                  'of its random-weight predictor, which are far more alike '
                                  'across query tiles than C2 uniform random scores'},
