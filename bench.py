@@ -17,9 +17,9 @@ with plain torch (:129-144, 315-333): the line carries the max error, a
 dense-match guard, and no TFLOP/s unless the error is within 2e-2.
 
 Reported beside it: "+prep" (selection, block mask and lists rebuilt per
-call), the full Veda layer (pooling of q, gather + pool of k, gather of v,
-predictor, selection, lists, sparse forward with the q permutation and the
-scatter fused in) on the same C2 patterns, the same layer with the lists of
+call), the full Veda layer (pooling of q and k, predictor, selection, lists,
+sparse forward reading q, k and v in sequence order with the scatter fused
+in) on the same C2 patterns, the same layer with the lists of
 its random-weight predictor (labelled as such), the dense baselines at the
 same shape, the roofline of the sparse kernel and the CPU baseline (the
 oracle's masked-dense attention + predictor on host cores).
