@@ -1952,11 +1952,31 @@ __global__ void __launch_bounds__(kStatThreads) tstats_kernel(FwdParams p) {
     dma16(b, 4 * wave < valid_of(e) ? koff : kskip, slot + wave * 1024);
   };
   // One step over the step's vch valid keys (sub-block B only when vch > 32).
+  // 'sum': once a row has a reference, the step's probabilities are taken
+  // against it as it stands and kept unless their sum could lose range
+  // (2^64 or more, or not finite), so most steps skip the row max; such a
+  // step, a row's first one, and every 'max' step run the online softmax as
+  // the sparse forward does (reference raised past a slack of 8).
   auto step = [&](const lds_u8* slot, int vch) {
     const f32x16 sa = sub_scores(slot, fa, w, vch, hi);
     f32x16 sb;
     const bool two = vch > 32;
     if (two) sb = sub_scores(slot, fb, w, vch - 32, hi);
+    if (HEAT == kHeatSum && __all(w.m_run != -INFINITY)) {
+      const float mu = w.mu;
+      float l4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        l4[e >> 2] += __builtin_amdgcn_exp2f(fmaf(sa[e], c, -mu));
+        if (two) l4[e >> 2] += __builtin_amdgcn_exp2f(fmaf(sb[e], c, -mu));
+      }
+      const float lsum = (l4[0] + l4[1]) + (l4[2] + l4[3]);
+      if (__all(lsum < 0x1p64f)) {
+        w.l_run += lsum;
+        w.blk += lsum;
+        return;
+      }
+    }
     float mloc = -INFINITY;
 #pragma unroll
     for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, two ? fmaxf(sa[e], sb[e]) : sa[e]);

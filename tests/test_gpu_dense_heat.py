@@ -75,6 +75,32 @@ def test_dense_heat_matches_oracle(reduce, with_v):
         assert out is None
 
 
+def test_dense_heat_sum_with_a_late_score_jump():
+    """'sum' keeps a row's reference while the step sums stay in range: a key
+    tile late in the walk whose scores jump far past every earlier one (K
+    scaled by 30: ~130 log2 units above the running max, so its
+    probabilities would overflow) makes those steps raise the reference, and
+    the LSE and heat still match the oracle on tile-ordered data."""
+    lay, olay, qt, kt, vt, _ = _case()
+    j = olay.n_video_tiles - 3
+    kt = kt.clone()
+    kt[j * 128:(j + 1) * 128] = (kt[j * 128:(j + 1) * 128].float() * 30).to(kt.dtype)
+    full = torch.ones(4, olay.n_tiles, olay.n_tiles, dtype=torch.bool)
+    _, ref_lse = oa.block_sparse_attention(qt, kt, vt, full, olay.valid_count, return_lse=True)
+    rows = torch.arange(0, olay.n_video_tiles)
+    heat, lse, _ = kernels.dense_heat(qt.cuda(), kt.cuda(), lay, rows.cuda(), 'sum')
+    heat, lse = heat.cpu(), lse.cpu()
+    sel = (rows[:, None] * 128 + torch.arange(128)[None, :]).reshape(-1)
+    real = _rows_valid(olay, rows)
+    want = ref_lse[:, sel]
+    torch.testing.assert_close(lse[:, real], want[:, real], rtol=0, atol=2e-4)
+    ref = oa.teacher_heat(qt, kt, ref_lse.t().contiguous(), olay, rows, 'sum',
+                          score_dtype=torch.float32)
+    torch.testing.assert_close(heat, ref, rtol=1e-4, atol=1e-7)
+    # the scaled tile takes most of the mass of many rows
+    assert (heat[:, :, j] > 0.5 * olay.valid_count[rows].float()).float().mean() > 0.1
+
+
 def test_dense_heat_head_chunks_and_empty_key_tile_are_exact():
     """Heads are independent: a workspace that forces one head per chunk
     gives the same bits. A key tile with no real row (valid count zeroed
