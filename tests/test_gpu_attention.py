@@ -367,6 +367,39 @@ def test_sequence_order_kv_entry_equals_gather_attend_scatter(name):
         kernels.block_sparse_attention_seq_kv_(got, q, k[:-1], v, lists, lay, heads)
 
 
+def test_sequence_order_kv_irregular_lists_keep_list_order():
+    """Lists whose members are reversed and that hold a void full-list entry
+    take list order in every form of the walk: the sequence-order entry
+    equals the tiled one bit for bit on them, and both stay within the
+    oracle's bar of the result on the regular lists."""
+    spec = helpers.small_layout()
+    lay = helpers.product_layout(*spec, device='cuda')
+    q, k, v = (t.cuda() for t in helpers.qkv(lay.seq_len, 4, 128, seed=7))
+    heads = torch.tensor([1, 3], device='cuda')
+    kt, vt = (kernels.gather_tiles(t, lay, heads) for t in (k, v))
+    g = torch.Generator().manual_seed(8)
+    mask = (torch.rand(2, lay.n_tiles, lay.n_tiles, generator=g) < 0.2) | torch.eye(
+        lay.n_tiles, dtype=torch.bool)[None]
+    pc, pi, fc, fi = kernels.index_lists(mask.cuda(), lay)
+    t = torch.arange(fi.shape[-1], device='cuda')
+    rev = lambda c, idx: idx.gather(-1, torch.where(t < c[..., None].long(),
+                                                    c[..., None].long() - 1 - t, t)).contiguous()
+    fir = rev(fc, fi).clone()
+    assert (fc < fir.shape[-1]).all()
+    fir.scatter_(-1, fc.long()[..., None], torch.full_like(fir[..., :1], lay.n_tiles + 7))
+    odd = (pc, rev(pc, pi), fc + 1, fir)
+    init = torch.zeros(lay.seq_len + 1, 4, 128, dtype=torch.bfloat16, device='cuda')
+    want, got, regular = init.clone(), init.clone(), init.clone()
+    kernels.block_sparse_attention_seq_(want, q, kt, vt, odd, lay, heads)
+    kernels.block_sparse_attention_seq_kv_(got, q, k, v, odd, lay, heads)
+    kernels.block_sparse_attention_seq_kv_(regular, q, k, v, (pc, pi, fc, fi), lay, heads)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16).cpu(), want.view(torch.int16).cpu())
+    d = (got.float() - regular.float())[:lay.used, [1, 3]]
+    assert d.abs().max().item() <= MAX_ABS
+    assert (d.norm() / regular.float()[:lay.used, [1, 3]].norm()).item() <= REL_L2
+
+
 def test_sequence_order_kv_non_finite_rows_stay_in_their_blocks():
     """With k / v read in sequence order a key tile's padding rows come from
     its first real row, so an Inf in that row's v reaches exactly the query
