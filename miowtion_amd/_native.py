@@ -13,6 +13,8 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / 'libveda_hip.so'
+# the signatures below are those of this ABI version (veda_abi_version())
+ABI_VERSION = 5
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int64
@@ -86,6 +88,12 @@ def load() -> ctypes.CDLL:
             lib.veda_last_error.restype = ctypes.c_char_p
             lib.veda_last_error.argtypes = []
             lib.veda_abi_version.restype = ctypes.c_int
+            lib.veda_abi_version.argtypes = []
+            found = lib.veda_abi_version()
+            if found != ABI_VERSION:
+                raise ImportError(
+                    f'{LIB_PATH} has ABI version {found}, this package binds version '
+                    f'{ABI_VERSION}: rebuild it with `python -m miowtion_amd.csrc.build`')
             _lib = lib
         return _lib
 

@@ -37,7 +37,7 @@ def test_library_built_and_exports_every_declared_symbol():
             continue
         assert len(_native.SIGNATURES[name]) == n, name
     assert set(_native.SIGNATURES) <= set(declared)
-    assert lib.veda_abi_version() == 5
+    assert lib.veda_abi_version() == _native.ABI_VERSION == 5
 
 
 def test_host_side_argument_checks():
