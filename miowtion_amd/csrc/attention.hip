@@ -47,6 +47,9 @@ constexpr int kD = 128;
 constexpr int kThreads = 512;
 constexpr int kTileBytes = kTile * kD * 2;       // 32 KB: one K or V tile
 constexpr int kMaxBlocks = 2048;                 // key tiles per row (FA4's cap)
+// LDS offset in ring slot 1 of the Q fragments a narrow walk hands from wave
+// 0 to wave 1 (8 KB, past the set-up's 12 KB step-list scratch)
+constexpr int kNarrowQ = 16384;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleSlack = 8.f;             // log2 units
 
@@ -143,6 +146,8 @@ struct WaveState {
 // step. The two key halves merge at the end.
 
 constexpr int kSlotBytes = 2 * kHalfBytes;      // 32 KB: K + V
+static_assert(3 * kMaxBlocks * 2 <= kNarrowQ && kNarrowQ + 8 * 64 * 16 <= kSlotBytes,
+              "narrow-walk Q fragments overlap the step-list scratch or leave the slot");
 
 // Per-lane byte offsets of the HBM -> LDS loads of one step. Wave w fills K
 // and V segments 2w, 2w + 1 (1 KB = rows 4 seg .. 4 seg + 3 of the half);
@@ -782,6 +787,81 @@ __device__ __forceinline__ void sstep_zero_q(const lds_u8* slot, const HFrag& fa
   sub_pv(slot, fb, kb, w);
 }
 
+// Narrow walk (a query tile whose only real rows are its first 32): each
+// wave takes one 32-key sub-block of every step, so the tile's products
+// spread over all four SIMDs of the workgroup instead of one wave's chain.
+// sstep_half is one sub-block (lim valid keys) of sstep for the tile's real
+// rows, with hook(k) before the fragment reads of score product k + 2;
+// sstep_half_zero is one sub-block of sstep_zero_q. The two sub-blocks'
+// partial states are merged at the end of the walk.
+template <typename Hook>
+__device__ __forceinline__ void sstep_half(const lds_u8* slot, const HFrag& f, float c, int lim,
+                                           int hi, WaveState& w, Hook hook) {
+  typedef const __attribute__((address_space(3))) u32x4* lds_u32x4;
+  f32x16 s;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) s[e] = 0.f;
+  u32x4 kf[8];
+  kf[0] = *reinterpret_cast<lds_u32x4>(slot + f.k[0]);
+  kf[1] = *reinterpret_cast<lds_u32x4>(slot + f.k[1]);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    hook(k);
+    if (k + 2 < 8) kf[k + 2] = *reinterpret_cast<lds_u32x4>(slot + f.k[k + 2]);
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[k]), w.qf[k], s, 0, 0, 0);
+  }
+  mask_scores(s, lim, hi);
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
+  mloc = half_swap_max(mloc) * c;
+  const float m_new = mloc > w.m_run + kRescaleSlack ? mloc : w.m_run;
+  const float mu = m_new == -INFINITY ? 0.f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(w.m_run - mu);
+  w.m_run = m_new;
+  float ps[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) ps[e] = __builtin_amdgcn_exp2f(fmaf(s[e], c, -mu));
+  float l4[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) l4[g] = (ps[4 * g] + ps[4 * g + 1]) + (ps[4 * g + 2] + ps[4 * g + 3]);
+  w.l_run = fmaf(w.l_run, alpha, (l4[0] + l4[1]) + (l4[2] + l4[3]));
+  u32x4 pk[2];
+  pack_probs(ps, pk);
+  if (__any(alpha != 1.f)) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) w.o[dt][e] *= alpha;
+  }
+  sub_pv(slot, f, pk, w);
+}
+
+__device__ __forceinline__ void sstep_half_zero(const lds_u8* slot, const HFrag& f, int lim, int hi,
+                                                WaveState& w) {
+  if (lim <= 0) return;  // no valid key: P is 0 everywhere
+  w.m_run = 0.f;
+  u32x4 pk[2];
+  if (lim >= 32) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) pk[kk] = u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+    w.l_run += 16.f;
+  } else {
+    // register e holds key 8 (e / 4) + 4 hi + e % 4 of the sub-block
+    float ps[16];
+    int n = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const bool v = 8 * (e >> 2) + 4 * hi + (e & 3) < lim;
+      ps[e] = v ? 1.f : 0.f;
+      n += v;
+    }
+    w.l_run += (float)n;
+    pack_probs(ps, pk);
+  }
+  sub_pv(slot, f, pk, w);
+}
+
 // The 16 weights of this lane's keys key0 + 8 g + 4 hi + m of a sub-block.
 __device__ __forceinline__ void sub_weights(const uint8_t* wt, int key0, int hi, float (&ww)[16]) {
 #pragma unroll
@@ -1258,6 +1338,15 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     }
     q_zero = __ballot(any != 0) == 0;
     if (MODE == kSparse && lane == 0) zflag[wave] = q_zero ? 1 : 0;
+    // wave 0's Q fragments for wave 1 of a narrow walk (below), in ring
+    // slot 1 past the step-list scratch; no load reaches slot 1 before the
+    // walk's first barrier
+    if (MODE == kSparse && wave == 0) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
+            (lds_u8*)ring[1] + kNarrowQ + (s * 64 + lane) * 16) = __builtin_bit_cast(u32x4, w.qf[s]);
+    }
   }
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -1276,6 +1365,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   // waves) only load and pass the barriers, then store its staged rows.
   int zero_src = 0;
   bool copy = false, has_copy = false;  // has_copy: workgroup-uniform
+  bool narrow = false;                  // workgroup-uniform
   if (MODE == kSparse) {
     const uint32_t zbits = __builtin_amdgcn_readfirstlane(
         (uint32_t)zflag[0] | ((uint32_t)zflag[1] << 1) | ((uint32_t)zflag[2] << 2) |
@@ -1283,8 +1373,29 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     zero_src = zbits ? __builtin_ctz(zbits) : 0;
     copy = q_zero && wave != zero_src;
     has_copy = __builtin_popcount(zbits) >= 2;
+    narrow = zbits == 0xEu;
   }
   const int n_lsteps = __builtin_amdgcn_readfirstlane(step_total);
+  // Narrow walk: only wave 0's rows are real (a tile with at most 32 valid
+  // rows). Wave 0 takes sub-block a of every step and wave 1 sub-block b,
+  // both for wave 0's rows (wave 1 takes wave 0's Q fragments from LDS);
+  // waves 2 and 3 take the all-zero rows' products of sub-blocks a and b.
+  // The halves merge after the walk; wave 2 then holds the all-zero rows'
+  // output and waves 1 and 3 copy it.
+  narrow = narrow && n_lsteps > 0;
+  if (narrow) {
+    zero_src = 2;
+    copy = (wave & 1) != 0;
+    if (wave == 1) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        w.qf[s] = as_bf16x8(*reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+            (const lds_u8*)ring[1] + kNarrowQ + (s * 64 + lane) * 16));
+      // read before this wave reaches the walk's first barrier, after which
+      // loads may target slot 1
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+  }
   const int n_small = LISTS ? __builtin_amdgcn_readfirstlane(step_small) : 0;
   const int n_steps = n_lsteps + n_virt;
 
@@ -1312,6 +1423,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   const float c = p.scale_log2;
   const SDma dma = sdma_offsets(p.ks, p.vs, wave, lane);
   const HFrag fa = hfrag_offsets(0, lane), fb = hfrag_offsets(1, lane);
+  const HFrag fh = hfrag_offsets(wave & 1, lane);  // a narrow walk's sub-block
   auto load_step = [&](int u, lds_u8* slot) {
     int64_t row0, rowb;
     int vch, lb;
@@ -1474,7 +1586,9 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     // eight waves of a CU queue at the load path together and each wave
     // stalls on them.
     // kind: 0 a wave with a real query row, 1 the wave that computes the
-    // all-zero groups' output, 2 a copy wave (loads only)
+    // all-zero groups' output, 2 a copy wave (loads only); in a narrow
+    // walk, 3 a wave with the tile's real rows over one sub-block and 4 the
+    // all-zero rows over one sub-block
     // Compensated attention: the last list step loads the first virtual
     // step (the tile summaries) instead.
     const bool virt_next = MODE == kSparseComp && n_virt > 0;
@@ -1484,7 +1598,11 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       const int la = (int)(ra & 63u), lb = (int)(rb & 63u);
       const char *kb, *vb;
       rec_base(na, nb, kb, vb);
-      if constexpr (decltype(kind)::value != 0) {
+      if constexpr (decltype(kind)::value == 3) {
+        sstep_half(cur, fh, c, (wave & 1) ? lb : la, hi, w, [&](int k) {
+          if (more) issue(kb, vb, k, nxt);
+        });
+      } else if constexpr (decltype(kind)::value != 0) {
         if (more) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) issue(kb, vb, j, nxt);
@@ -1493,6 +1611,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
           for (int j = 0; j < 8; ++j) virtual_seg(0, nxt_slot, j);
         }
         if constexpr (decltype(kind)::value == 1) sstep_zero_q(cur, fa, fb, la, lb, hi, w);
+        if constexpr (decltype(kind)::value == 4) sstep_half_zero(cur, fh, (wave & 1) ? lb : la, hi, w);
       } else {
         sstep(cur, fa, fb, c, la, lb, hi, w, [&](int k) {
           if (more) issue(kb, vb, k, nxt);
@@ -1583,12 +1702,17 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
                        const uint32_t (&ok)[4], const uint32_t (&ov)[4], uint32_t nxt)
         __attribute__((always_inline)) {
       const int la = (int)(ra & 63u), lb = (int)(rb & 63u);
-      if constexpr (decltype(kind)::value != 0) {
+      if constexpr (decltype(kind)::value == 3) {
+        sstep_half(cur, fh, c, (wave & 1) ? lb : la, hi, w, [&](int k) {
+          if (more) issue_kv(ok, ov, k, nxt);
+        });
+      } else if constexpr (decltype(kind)::value != 0) {
         if (more) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) issue_kv(ok, ov, j, nxt);
         }
         if constexpr (decltype(kind)::value == 1) sstep_zero_q(cur, fa, fb, la, lb, hi, w);
+        if constexpr (decltype(kind)::value == 4) sstep_half_zero(cur, fh, (wave & 1) ? lb : la, hi, w);
       } else {
         sstep(cur, fa, fb, c, la, lb, hi, w, [&](int k) {
           if (more) issue_kv(ok, ov, k, nxt);
@@ -1642,14 +1766,22 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       }
     };
     if constexpr (SEQKV) {
-      if (copy)
+      if (narrow && wave < 2)
+        walk_kv(std::integral_constant<int, 3>{});
+      else if (narrow)
+        walk_kv(std::integral_constant<int, 4>{});
+      else if (copy)
         walk_kv(std::integral_constant<int, 2>{});
       else if (q_zero)
         walk_kv(std::integral_constant<int, 1>{});
       else
         walk_kv(std::integral_constant<int, 0>{});
     } else {
-      if (copy)
+      if (narrow && wave < 2)
+        walk(std::integral_constant<int, 3>{});
+      else if (narrow)
+        walk(std::integral_constant<int, 4>{});
+      else if (copy)
         walk(std::integral_constant<int, 2>{});
       else if (q_zero)
         walk(std::integral_constant<int, 1>{});
@@ -1742,6 +1874,50 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     }
   }
   }  // the dense walk and the compensation of a given output
+
+  if (MODE == kSparse && narrow) {
+    // Merge the narrow walk's halves: wave 1's state (the real rows over
+    // sub-block b) into wave 0's, wave 3's (the all-zero rows over b) into
+    // wave 2's, through the last step's slot once every wave is done with
+    // it. Lane l of a pair holds the same row and keys on both sides;
+    // each side's O and l are relative to its own reference m, so both
+    // move to the larger one (a side with no valid key has m = -inf and
+    // weighs 0). The zero rows' state is the same for every row, so wave 3
+    // passes one row's (lanes 0 and 32).
+    float* xo = reinterpret_cast<float*>(ring[(n_steps - 1) & 1]);
+    float* xz = xo + 66 * 64;
+    __syncthreads();
+    if (wave == 1) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xo[(16 * dt + e) * 64 + lane] = w.o[dt][e];
+      xo[64 * 64 + lane] = w.m_run;
+      xo[65 * 64 + lane] = w.l_run;
+    } else if (wave == 3 && li == 0) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xz[(16 * dt + e) * 2 + hi] = w.o[dt][e];
+      xz[128 + hi] = w.m_run;
+      xz[130 + hi] = w.l_run;
+    }
+    __syncthreads();
+    if (wave == 0 || wave == 2) {
+      const int ix = wave == 0 ? lane : hi, n = wave == 0 ? 64 : 2;
+      const float* src = wave == 0 ? xo : xz;
+      const float mb = src[64 * n + ix], lb = src[65 * n + ix];
+      const float m = fmaxf(w.m_run, mb);
+      const float mu = m == -INFINITY ? 0.f : m;
+      const float aa = __builtin_amdgcn_exp2f(w.m_run - mu), ab = __builtin_amdgcn_exp2f(mb - mu);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) w.o[dt][e] = w.o[dt][e] * aa + src[(16 * dt + e) * n + ix] * ab;
+      w.l_run = w.l_run * aa + lb * ab;
+      w.m_run = m;
+    }
+  }
 
   const float l = half_swap_sum(w.l_run);
   // compensation: the kept output is num / den over the kept keys with

@@ -135,6 +135,50 @@ def test_all_zero_query_groups_match_the_oracle_on_every_row():
     _close(lse.T, ref_lse.T)
 
 
+def test_narrow_walk_tiles_match_the_oracle_on_every_row():
+    """Query tiles whose only non-zero rows are their first 32 take the
+    narrow walk (one 32-key sub-block of every step per wave, the halves
+    merged at the end). Made here by zeroing rows 32..127 of several tiles:
+    one with all 32 first rows real, one with 24, one that keeps a single
+    ragged key tile (its step's second sub-block has no valid key), one that
+    keeps a single full key tile and one that keeps nothing. Every row
+    (padding included) and the LSE against the oracle, in tile order and
+    through the sequence-order entry with k and v in sequence order."""
+    spec = helpers.small_layout(grid=(5, 12, 20), shape='2x8x8')
+    lay, olay, qt, kt, vt, mask = _case(spec, heads=2, ratio=0.4, seed=11)
+    vc = olay.valid_count
+    ragged = int(torch.nonzero((vc > 0) & (vc <= 32)).flatten()[0])
+    full = int(torch.nonzero(vc == 128).flatten()[0])
+    tiles = [int(t) for t in torch.nonzero(vc == 128).flatten()[:5]]
+    qt = qt.clone()
+    for t in tiles:
+        qt[t * 128 + 32:(t + 1) * 128] = 0
+    qt[tiles[1] * 128 + 24:tiles[1] * 128 + 32] = 0
+    mask[:, tiles[2]] = False
+    mask[:, tiles[2], ragged] = True
+    mask[:, tiles[3]] = False
+    mask[:, tiles[3], full] = True
+    mask[1, tiles[4]] = False
+    out, lse = kernels.block_sparse_attention(qt.cuda(), kt.cuda(), vt.cuda(), mask.cuda(), lay,
+                                              return_lse=True)
+    ref, ref_lse = oa.block_sparse_attention(qt, kt, vt, mask, olay.valid_count, return_lse=True)
+    _close(out, ref)
+    _close(lse.T, ref_lse.T)
+    rows = torch.cat([torch.arange(t * 128, (t + 1) * 128) for t in tiles])
+    _close(out, ref, rows)
+    # the sequence-order entry (q, k, v in sequence order, output scattered)
+    perm = olay.perm
+    ok = perm >= 0
+    qs, ks, vs = (torch.zeros(lay.seq_len, 2, 128, dtype=torch.bfloat16) for _ in range(3))
+    qs[perm[ok]], ks[perm[ok]], vs[perm[ok]] = qt[ok], kt[ok], vt[ok]
+    lists = kernels.index_lists(mask.cuda(), lay)
+    got = torch.zeros(lay.seq_len + 1, 2, 128, dtype=torch.bfloat16, device='cuda')
+    kernels.block_sparse_attention_seq_kv_(got, qs.cuda(), ks.cuda(), vs.cuda(), lists, lay, None)
+    want = torch.zeros(lay.seq_len, 2, 128, dtype=torch.bfloat16)
+    want[perm[ok]] = out.cpu()[ok]
+    assert torch.equal(got[:-1].cpu().view(torch.int16), want.view(torch.int16))
+
+
 def test_query_tile_subset_rows():
     """q holds only some query tiles; mask rows follow q (fa4.py:308-313)."""
     lay, olay, qt, kt, vt, mask = _case(helpers.small_layout(), seed=3)
