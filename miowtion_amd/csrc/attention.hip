@@ -972,6 +972,37 @@ __device__ __forceinline__ void vstep_fixed(const lds_u8* slot, const HFrag& fa,
 #undef VEDA_FENCE
 }
 
+// vstep_fixed for a wave whose 32 query rows are all zero: every virtual
+// key scores exactly 0, so p = exp2(-ref2) (x0, per row) wherever the
+// key's weight is positive; only the P.V products remain. Same products,
+// probabilities and den sums in the same order as vstep_fixed, so the
+// result is the same bit for bit.
+__device__ __forceinline__ void vstep_fixed_zero(const lds_u8* slot, const HFrag& fa,
+                                                 const HFrag& fb, const uint8_t* wt, int key0,
+                                                 int hi, float x0, WaveState& w) {
+  auto sub = [&](const HFrag& f, int k0) {
+    u32x4 pk[2];
+    float den = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t w4 = *reinterpret_cast<const uint32_t*>(wt + k0 + 8 * g + 4 * hi);
+      float ps[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const float ww = (float)((w4 >> (8 * m)) & 0xffu);
+        ps[m] = ww > 0.f ? x0 : 0.f;
+        den = fmaf(ps[m], ww, den);
+      }
+      pk[g >> 1][2 * (g & 1)] = pack_bf16x2(ps[0], ps[1]);
+      pk[g >> 1][2 * (g & 1) + 1] = pack_bf16x2(ps[2], ps[3]);
+    }
+    w.l_run += den;
+    sub_pv(slot, f, pk, w);
+  };
+  sub(fa, key0);
+  sub(fb, key0 + 32);
+}
+
 // One step of 64 virtual keys inside the online softmax (compensated
 // attention): as sstep, with each key weighted by its tile's dropped
 // real-row count (the denominator gains p * weight; the value is the
@@ -1329,7 +1360,7 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   // a wave whose 32 query rows are all zero (padding rows) takes the
   // product-free step (wave-uniform)
   bool q_zero = false;
-  if (MODE == kSparse || MODE == kSparseComp) {
+  if (MODE == kSparse || MODE == kSparseComp || MODE == kVirtualOnly) {
     uint32_t any = 0;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
@@ -1860,18 +1891,33 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   } else {
     // compensation of a given output: the virtual steps, step u in slot
     // u % 2 (step 0's loads went out at set-up), unrolled by two so that
-    // every fragment read has a constant slot address
-    int u = 0;
-    for (; u + 1 < n_steps; u += 2) {
-      begin_step(u, s1);
-      virtual_step(u, s0);
-      begin_step(u + 1, s0);
-      virtual_step(u + 1, s1);
-    }
-    if (u < n_steps) {
-      begin_step(u, s1);
-      virtual_step(u, s0);
-    }
+    // every fragment read has a constant slot address. A wave whose 32
+    // query rows are all zero takes the product-free step (one copy of the
+    // loop per kind, so O stays in one set of registers).
+    auto vwalk = [&](auto zero) __attribute__((always_inline)) {
+      const float x0 = __builtin_amdgcn_exp2f(-ref2);
+      auto vstep = [&](int v, const lds_u8* cur) __attribute__((always_inline)) {
+        if constexpr (decltype(zero)::value)
+          vstep_fixed_zero(cur, fa, fb, vwt, v * kHalf, hi, x0, w);
+        else
+          virtual_step(v, cur);
+      };
+      int u = 0;
+      for (; u + 1 < n_steps; u += 2) {
+        begin_step(u, s1);
+        vstep(u, s0);
+        begin_step(u + 1, s0);
+        vstep(u + 1, s1);
+      }
+      if (u < n_steps) {
+        begin_step(u, s1);
+        vstep(u, s0);
+      }
+    };
+    if (MODE == kVirtualOnly && q_zero)
+      vwalk(std::true_type{});
+    else
+      vwalk(std::false_type{});
   }
   }  // the dense walk and the compensation of a given output
 
