@@ -369,34 +369,48 @@ def suite(reps: int = 5) -> dict:
 def _backward(c: dict, kept: int, steps: int, warmup: int) -> int:
     """The block-sparse backward at C2 given the forward's out and LSE (one
     veda_block_sparse_bwd call: stats, dQ and dK/dV kernels); TFLOP/s on 5
-    products of 2 * 128^3 per kept block."""
+    products of 2 * 128^3 per kept block. Timed with two output gradients:
+    the one a layer's scatter passes back (N(0, 1) on real rows, 0 on the
+    padding rows of partial query tiles, whose outputs the scatter drops:
+    the line's value), and N(0, 1) on every row, padding included."""
     from miowtion_amd import kernels, ops
     lay = c['lay']
     lists_t = kernels.index_lists(c['mask'], lay, transpose=True)
     o, lse = kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'], c['lists'], lay,
                                                   return_lse=True)
-    dout = torch.randn(o.shape, generator=torch.Generator(device='cuda').manual_seed(3),
-                       device='cuda').to(torch.bfloat16)
+    dout_all = torch.randn(o.shape, generator=torch.Generator(device='cuda').manual_seed(3),
+                           device='cuda').to(torch.bfloat16)
+    dout_layer = dout_all * lay.slot_valid.to(dout_all.dtype)[:, None, None]
 
-    def step():
-        return ops.block_sparse_bwd(c['qt'], c['kt'], c['vt'], o, dout, lse, None, *c['lists'],
-                                    *lists_t, lay.valid_count,
-                                    lay.n_tiles - lay.n_video_tiles)
+    def timed(dout):
+        def step():
+            return ops.block_sparse_bwd(c['qt'], c['kt'], c['vt'], o, dout, lse, None, *c['lists'],
+                                        *lists_t, lay.valid_count,
+                                        lay.n_tiles - lay.n_video_tiles)
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        ms = sorted(_events_ms(step, max(5, steps)))
+        return ms[len(ms) // 2], sum(ms) / len(ms)
 
-    _log(f'bench: backward, warmup {warmup}')
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    _log(f'bench: backward, timing {steps} steps')
-    ms = sorted(_events_ms(step, max(5, steps)))
-    med, avg = ms[len(ms) // 2], sum(ms) / len(ms)
+    _log(f'bench: backward, warmup {warmup}, timing {steps} steps, layer gradient')
+    med, avg = timed(dout_layer)
+    _log('bench: backward, gradient on every row')
+    med_all, avg_all = timed(dout_all)
     flop = 10.0 * 128 * 128 * D * kept
+    tf = lambda ms: round(flop / (ms * 1e-3) / 1e12, 2)
     print(json.dumps({'metric': 'block-sparse attention backward TFLOP/s @C2 (5 products per '
                                 'kept block)',
-                      'value': round(flop / (med * 1e-3) / 1e12, 2), 'ms_per_step': round(med, 4),
+                      'value': tf(med), 'ms_per_step': round(med, 4),
                       'avg_launch_ms': round(avg, 4), 'flop_per_launch': flop,
-                      'frac_of_bf16_peak': round(flop / (med * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                      'kept_blocks': kept}), flush=True)
+                      'frac_of_bf16_peak': round(tf(med) / PEAK_BF16_TFLOPS, 4),
+                      'kept_blocks': kept,
+                      'dout': 'layer gradient: N(0,1) on real rows, 0 on padding rows (the '
+                              'scatter drops their outputs)',
+                      'dout_every_row': {'value': tf(med_all), 'ms_per_step': round(med_all, 4),
+                                         'avg_launch_ms': round(avg_all, 4),
+                                         'frac_of_bf16_peak': round(tf(med_all) / PEAK_BF16_TFLOPS,
+                                                                    4)}}), flush=True)
     return 0
 
 

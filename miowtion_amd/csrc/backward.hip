@@ -50,7 +50,9 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kMaxTiles = 2048;                  // tiles per list row (FA4's cap)
-constexpr int kRecFloats = 256;                  // stats record: 64 lse2, 64 D, 128 zero
+constexpr int kRecFloats = 256;                  // stats record: 64 lse2, 64 -D, the zero
+                                                 // flag, zeros
+constexpr int kZeroFlag = 128;                   // 1 if every row has dO = 0 and D = 0
 constexpr int kRecBytes = kRecFloats * 4;
 constexpr int kDqThreads = 256;
 constexpr int kDkvThreads = 512;
@@ -159,8 +161,9 @@ __device__ __forceinline__ void pack_b(const float (&x)[16], u32x4 (&pk)[2]) {
 }
 
 // Wave 0 of a workgroup: the steps (target << 1 | half) of the full list,
-// then of the partial list, in list order; halves(t) = how many 64-row
-// halves of target t are steps (0 drops the entry). Returns the count.
+// then of the partial list, in list order; halves(t) = which 64-row halves
+// of target t are steps (bit 0: the first, bit 1: the second; 0 drops the
+// entry). Returns the count.
 template <class Halves>
 __device__ int build_steps(const int32_t* fl, int nf, const int32_t* pl, int np, int lane,
                            uint16_t* steps, Halves halves) {
@@ -173,12 +176,13 @@ __device__ int build_steps(const int32_t* fl, int nf, const int32_t* pl, int np,
       t = i < nf ? fl[i] : pl[i - nf];
       h = halves(t);
     }
-    const uint64_t b0 = __ballot(h >= 1), b1 = __ballot(h >= 2);
+    const bool h0 = (h & 1) != 0, h1 = (h & 2) != 0;
+    const uint64_t b0 = __ballot(h0), b1 = __ballot(h1);
     const int rank =
         __builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0)) +
         __builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0));
-    if (h >= 1) steps[n + rank] = (uint16_t)(t << 1);
-    if (h >= 2) steps[n + rank + 1] = (uint16_t)((t << 1) | 1);
+    if (h0) steps[n + rank] = (uint16_t)(t << 1);
+    if (h1) steps[n + rank + (int)h0] = (uint16_t)((t << 1) | 1);
     n += __builtin_popcountll(b0) + __builtin_popcountll(b1);
   }
   return n;
@@ -202,12 +206,14 @@ __global__ void __launch_bounds__(256) bwd_stats_kernel(BwdParams p) {
   const int64_t head = rec / per_head, st = rec % per_head;
   const int tid = threadIdx.x, sub = tid & 15;
   float* out = p.stats + rec * kRecFloats;
+  bool live = false;  // a non-zero dO element or D among this thread's
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int rr = 16 * it + (tid >> 4);
     const int64_t row = st * 64 + rr;
     const u32x4 a = ld16(p.o + row * p.os + head * p.oh + 8 * sub);
     const u32x4 b = ld16(p.dout + row * p.dos + head * p.doh + 8 * sub);
+    live |= ((b[0] | b[1] | b[2] | b[3]) & 0x7FFF7FFFu) != 0;  // +-0 count as zero
     float acc = 0.f;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -221,10 +227,13 @@ __global__ void __launch_bounds__(256) bwd_stats_kernel(BwdParams p) {
     if (sub == 0) {
       const float l = p.lse[head * p.lse_sh + row * p.lse_ss];
       out[rr] = l == -INFINITY ? INFINITY : l * kLog2e;
-      out[64 + rr] = p.dlse != nullptr ? p.dlse[head * p.dlse_sh + row * p.dlse_ss] - acc : -acc;
+      const float nd = p.dlse != nullptr ? p.dlse[head * p.dlse_sh + row * p.dlse_ss] - acc : -acc;
+      out[64 + rr] = nd;
+      live |= nd != 0.f;  // NaN too
     }
   }
-  if (tid < 128) out[128 + tid] = 0.f;
+  const bool zero = __syncthreads_and(!live) != 0;
+  if (tid < 128) out[kZeroFlag + tid] = tid == 0 && zero ? 1.f : 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -258,7 +267,7 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
                               lane, steps, [&](int t) {
                                 if (t < 0 || t >= nk) return 0;
                                 const int vc = clamp_vc(p.valid_count[t]);
-                                return vc > kHalf ? 2 : vc > 0 ? 1 : 0;
+                                return vc > kHalf ? 3 : vc > 0 ? 1 : 0;
                               });
     if (lane == 0) step_total = n;
   }
@@ -273,11 +282,20 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
   const float lse2 = rec[(32 * wave + li) & 63];
   // -D of this lane's row, the initial accumulator of its dP products
   f32x16 neg_d;
-  {
-    const float nd = rec[64 + ((32 * wave + li) & 63)];
+  const float nd = rec[64 + ((32 * wave + li) & 63)];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) neg_d[e] = nd;
+  for (int e = 0; e < 16; ++e) neg_d[e] = nd;
+  // A wave whose 32 rows all have dO = 0 and D = 0 (the padding rows of a
+  // partial query tile when the caller's gradient comes through the
+  // scatter, which drops them): dP - D and dS are exactly 0 there, so its
+  // dQ rows are 0 and it only loads and passes the barriers (wave-uniform)
+  uint32_t live = nd != 0.f ? 1u : 0u;  // NaN too
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const u32x4 x = __builtin_bit_cast(u32x4, dof[s]);
+    live |= ((x[0] | x[1] | x[2] | x[3]) & 0x7FFF7FFFu) != 0 ? 1u : 0u;
   }
+  const bool d_zero = __ballot(live != 0) == 0;
   f32x16 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -397,7 +415,7 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
   // (every wave's loads of step u are in LDS and every wave is done reading
   // the other slot), issue step u + 1 into the other slot, compute step u.
   // The list reads stay above the barrier, out of the products' schedule.
-  auto run = [&](int u, lds_u8* cur, lds_u8* nxt) {
+  auto run = [&](auto zero, int u, lds_u8* cur, lds_u8* nxt) __attribute__((always_inline)) {
     const int t = entry(u);
     const int vc = __builtin_amdgcn_readfirstlane((int)tvc[t >> 1]);
     const int vch = t & 1 ? vc - kHalf : min(vc, kHalf);  // valid keys of the step
@@ -412,19 +430,33 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
     const int64_t row0 = (int64_t)(tn >> 1) * kTile + (tn & 1) * kHalf;
     const char* kb = reinterpret_cast<const char*>(kbase + row0 * p.ks);
     const char* vb = reinterpret_cast<const char*>(vbase + row0 * p.vs);
-    compute(vch, cur, [&](int s) {
+    auto hook = [&](int s) {
       if (more) {
         if (s < 4) dma16(kb, koff[s], nxt + (4 * wave + s) * 1024);
         else dma16(vb, voff[s - 4], nxt + kHalfBytes + (4 * wave + s - 4) * 1024);
       }
-    });
+    };
+    if constexpr (decltype(zero)::value) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) hook(s);
+    } else {
+      compute(vch, cur, hook);
+    }
+  };
+  // one copy of the walk per kind of wave (the same loads and barriers), so
+  // the accumulators stay in one set of registers
+  auto walk = [&](auto zero) __attribute__((always_inline)) {
+    for (int u = 0; u < n_steps; u += 2) {
+      run(zero, u, s0, s1);
+      if (u + 1 >= n_steps) break;
+      run(zero, u + 1, s1, s0);
+    }
   };
   if (n_steps > 0) load_step(entry(0), s0);
-  for (int u = 0; u < n_steps; u += 2) {
-    run(u, s0, s1);
-    if (u + 1 >= n_steps) break;
-    run(u + 1, s1, s0);
-  }
+  if (d_zero)
+    walk(std::true_type{});
+  else
+    walk(std::false_type{});
 
   // dQ leaves as whole rows: each wave writes its 32 bf16 rows into its
   // 8 KB of the slot no step reads any more (the last step's is
@@ -521,9 +553,17 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
     const int64_t lr = head * p.n_k_tiles + j;
     int nf, np;
     list_counts(p.full_cnt_t, p.part_cnt_t, lr, p.list_ld_t, nf, np);
+    // a 64-row half whose rows all have dO = 0 and D = 0 (the padding rows
+    // of a partial query tile when the caller's gradient comes through the
+    // scatter, which drops them) adds exactly zero to dK and dV: no step
+    const float* zrec = p.stats + head * 2 * p.n_q_tiles * kRecFloats + kZeroFlag;
     const int cnt = build_steps(p.full_idx_t + lr * p.list_ld_t, nf,
-                                p.part_idx_t + lr * p.list_ld_t, np, lane, steps,
-                                [&](int t) { return (vc > 0 && t >= 0 && t < nq) ? 2 : 0; });
+                                p.part_idx_t + lr * p.list_ld_t, np, lane, steps, [&](int t) {
+                                  if (vc <= 0 || t < 0 || t >= nq) return 0;
+                                  const bool z0 = zrec[(2 * t) * kRecFloats] != 0.f;
+                                  const bool z1 = zrec[(2 * t + 1) * kRecFloats] != 0.f;
+                                  return (z0 ? 0 : 1) | (z1 ? 0 : 2);
+                                });
     if (lane == 0) step_total = cnt;
   }
   f32x4 acc_v[8], acc_k[8];

@@ -115,6 +115,34 @@ def test_lse_gradient():
         _bar(t.grad, w, name)
 
 
+def test_zero_gradient_rows_are_skipped_exactly():
+    """A layer's gradient through the scatter is zero on padding rows. A
+    64-row half whose rows all have dO = 0 and D = 0 adds exactly zero to
+    dK and dV (the dK/dV walk drops its step), and a dQ wave whose 32 rows
+    all have them computes nothing (its rows are 0). Here: dO zero on every
+    padding row, on the second half of one full query tile and on a whole
+    32-row group of another, and on the second half of a third tile where
+    one row has a non-zero LSE gradient (D != 0: that half must still
+    count). Every gradient against the oracle."""
+    lay, olay, qt, kt, vt, mask, grad_out = _ref_case(4, ratio=0.5)
+    real = olay.slot_valid.bool().cuda()
+    dout = grad_out * real.to(grad_out.dtype)[:, None, None]
+    full = [int(t) for t in torch.nonzero(olay.valid_count == 128).flatten()[:3]]
+    assert (olay.valid_count <= 64).any()  # a padding half: a dropped step
+    dout[full[0] * 128 + 64:(full[0] + 1) * 128] = 0
+    dout[full[1] * 128 + 32:full[1] * 128 + 64] = 0
+    dout[full[2] * 128 + 64:(full[2] + 1) * 128] = 0
+    dlse = torch.zeros(4, qt.shape[0], device='cuda')
+    dlse[1, full[2] * 128 + 100] = 0.75
+    got = _gpu_grads(qt, kt, vt, mask, lay, dout, dlse)
+    want = _oracle_grads(qt, kt, vt, mask, olay, dout, dlse)
+    for name, g, w in zip('qkv', got, want):
+        _bar(g, w, name)
+    # rows whose dO and D are zero get dQ exactly 0
+    zq = got[0].cpu()[full[1] * 128 + 32:full[1] * 128 + 64]
+    assert (zq == 0).all()
+
+
 def test_transposed_lists_bit_exact():
     lay, olay, qt, kt, vt, mask, grad_out = _ref_case(3)
     got = kernels.index_lists(mask, lay, transpose=True)
