@@ -53,6 +53,7 @@ constexpr int kMaxTiles = 2048;                  // tiles per list row (FA4's ca
 constexpr int kRecFloats = 256;                  // stats record: 64 lse2, 64 -D, the zero
                                                  // flag, zeros
 constexpr int kZeroFlag = 128;                   // 1 if every row has dO = 0 and D = 0
+constexpr int kHiZeroFlag = 129;                 // 1 if rows 32 .. 63 have dO = 0 and D = 0
 constexpr int kRecBytes = kRecFloats * 4;
 constexpr int kDqThreads = 256;
 constexpr int kDkvThreads = 512;
@@ -163,12 +164,19 @@ __device__ __forceinline__ void pack_b(const float (&x)[16], u32x4 (&pk)[2]) {
 // Wave 0 of a workgroup: the steps (target << 1 | half) of the full list,
 // then of the partial list, in list order; halves(t) = which 64-row halves
 // of target t are steps (bit 0: the first, bit 1: the second; 0 drops the
-// entry). Returns the count.
+// entry) and which of those are "upper-zero" steps (bit 2: the first, bit 3:
+// the second), which go to the back of `steps` (entry k of them at
+// 2 kMaxTiles - 1 - k), also in list order. Returns the count of the others;
+// n_hz receives the count of the upper-zero steps.
 template <class Halves>
 __device__ int build_steps(const int32_t* fl, int nf, const int32_t* pl, int np, int lane,
-                           uint16_t* steps, Halves halves) {
-  int n = 0;
+                           uint16_t* steps, Halves halves, int& n_hz) {
+  int n = 0, nz = 0;
   const int total = nf + np;
+  auto below = [](uint64_t b) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0));
+  };
   for (int i0 = 0; i0 < total; i0 += 64) {
     const int i = i0 + lane;
     int t = 0, h = 0;
@@ -176,15 +184,18 @@ __device__ int build_steps(const int32_t* fl, int nf, const int32_t* pl, int np,
       t = i < nf ? fl[i] : pl[i - nf];
       h = halves(t);
     }
-    const bool h0 = (h & 1) != 0, h1 = (h & 2) != 0;
-    const uint64_t b0 = __ballot(h0), b1 = __ballot(h1);
-    const int rank =
-        __builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0)) +
-        __builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0));
-    if (h0) steps[n + rank] = (uint16_t)(t << 1);
-    if (h1) steps[n + rank + (int)h0] = (uint16_t)((t << 1) | 1);
-    n += __builtin_popcountll(b0) + __builtin_popcountll(b1);
+    const bool f0 = (h & 1) && !(h & 4), f1 = (h & 2) && !(h & 8);  // the others
+    const bool z0 = (h & 1) && (h & 4), z1 = (h & 2) && (h & 8);    // upper-zero
+    const uint64_t bf0 = __ballot(f0), bf1 = __ballot(f1), bz0 = __ballot(z0), bz1 = __ballot(z1);
+    const int rf = n + below(bf0) + below(bf1), rz = nz + below(bz0) + below(bz1);
+    if (f0) steps[rf] = (uint16_t)(t << 1);
+    if (f1) steps[rf + (int)f0] = (uint16_t)((t << 1) | 1);
+    if (z0) steps[2 * kMaxTiles - 1 - rz] = (uint16_t)(t << 1);
+    if (z1) steps[2 * kMaxTiles - 1 - (rz + (int)z0)] = (uint16_t)((t << 1) | 1);
+    n += __builtin_popcountll(bf0) + __builtin_popcountll(bf1);
+    nz += __builtin_popcountll(bz0) + __builtin_popcountll(bz1);
   }
+  n_hz = nz;
   return n;
 }
 
@@ -206,14 +217,16 @@ __global__ void __launch_bounds__(256) bwd_stats_kernel(BwdParams p) {
   const int64_t head = rec / per_head, st = rec % per_head;
   const int tid = threadIdx.x, sub = tid & 15;
   float* out = p.stats + rec * kRecFloats;
-  bool live = false;  // a non-zero dO element or D among this thread's
+  bool live = false, live_hi = false;  // a non-zero dO element or D among this thread's
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int rr = 16 * it + (tid >> 4);
     const int64_t row = st * 64 + rr;
     const u32x4 a = ld16(p.o + row * p.os + head * p.oh + 8 * sub);
     const u32x4 b = ld16(p.dout + row * p.dos + head * p.doh + 8 * sub);
-    live |= ((b[0] | b[1] | b[2] | b[3]) & 0x7FFF7FFFu) != 0;  // +-0 count as zero
+    const bool nz = ((b[0] | b[1] | b[2] | b[3]) & 0x7FFF7FFFu) != 0;  // +-0 count as zero
+    live |= nz;
+    if (it >= 2) live_hi |= nz;
     float acc = 0.f;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -230,10 +243,13 @@ __global__ void __launch_bounds__(256) bwd_stats_kernel(BwdParams p) {
       const float nd = p.dlse != nullptr ? p.dlse[head * p.dlse_sh + row * p.dlse_ss] - acc : -acc;
       out[64 + rr] = nd;
       live |= nd != 0.f;  // NaN too
+      if (it >= 2) live_hi |= nd != 0.f;
     }
   }
   const bool zero = __syncthreads_and(!live) != 0;
-  if (tid < 128) out[kZeroFlag + tid] = tid == 0 && zero ? 1.f : 0.f;
+  const bool zero_hi = __syncthreads_and(!live_hi) != 0;
+  if (tid < 128)
+    out[kZeroFlag + tid] = (tid == 0 && zero) || (tid == 1 && zero_hi) ? 1.f : 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -263,12 +279,13 @@ __global__ void __launch_bounds__(kDqThreads, 2) dq_kernel(BwdParams p) {
     const int64_t lr = head * p.n_q_tiles + r;
     int nf, np;
     list_counts(p.full_cnt, p.part_cnt, lr, p.list_ld, nf, np);
+    int n_hz;  // always 0 here
     const int n = build_steps(p.full_idx + lr * p.list_ld, nf, p.part_idx + lr * p.list_ld, np,
                               lane, steps, [&](int t) {
                                 if (t < 0 || t >= nk) return 0;
                                 const int vc = clamp_vc(p.valid_count[t]);
                                 return vc > kHalf ? 3 : vc > 0 ? 1 : 0;
-                              });
+                              }, n_hz);
     if (lane == 0) step_total = n;
   }
 
@@ -540,7 +557,7 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) dkv_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[2][kSlot + kRecBytes];
   __shared__ uint16_t steps[2 * kMaxTiles];
-  __shared__ int32_t step_total;
+  __shared__ int32_t step_total, step_hz;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, g = lane >> 4;
@@ -553,24 +570,38 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
     const int64_t lr = head * p.n_k_tiles + j;
     int nf, np;
     list_counts(p.full_cnt_t, p.part_cnt_t, lr, p.list_ld_t, nf, np);
-    // a 64-row half whose rows all have dO = 0 and D = 0 (the padding rows
+    // A 64-row half whose rows all have dO = 0 and D = 0 (the padding rows
     // of a partial query tile when the caller's gradient comes through the
-    // scatter, which drops them) adds exactly zero to dK and dV: no step
+    // scatter, which drops them) adds exactly zero to dK and dV: no step. One
+    // whose rows 32 .. 63 alone have them is an upper-zero step: only its
+    // first 32 rows are computed, in a second walk after the others.
     const float* zrec = p.stats + head * 2 * p.n_q_tiles * kRecFloats + kZeroFlag;
+    int n_hz;
     const int cnt = build_steps(p.full_idx_t + lr * p.list_ld_t, nf,
                                 p.part_idx_t + lr * p.list_ld_t, np, lane, steps, [&](int t) {
                                   if (vc <= 0 || t < 0 || t >= nq) return 0;
-                                  const bool z0 = zrec[(2 * t) * kRecFloats] != 0.f;
-                                  const bool z1 = zrec[(2 * t + 1) * kRecFloats] != 0.f;
-                                  return (z0 ? 0 : 1) | (z1 ? 0 : 2);
-                                });
-    if (lane == 0) step_total = cnt;
+                                  const float* r0 = zrec + (2 * t) * kRecFloats;
+                                  const float* r1 = r0 + kRecFloats;
+                                  constexpr int h = kHiZeroFlag - kZeroFlag;
+                                  return (r0[0] != 0.f ? 0 : 1) | (r1[0] != 0.f ? 0 : 2) |
+                                         (r0[h] != 0.f ? 4 : 0) | (r1[h] != 0.f ? 8 : 0);
+                                }, n_hz);
+    if (lane == 0) {
+      step_total = cnt;
+      step_hz = n_hz;
+    }
   }
   f32x4 acc_v[8], acc_k[8];
 #pragma unroll
   for (int db = 0; db < 8; ++db) acc_v[db] = acc_k[db] = f32x4{0.f, 0.f, 0.f, 0.f};
   __syncthreads();
-  const int n_steps = __builtin_amdgcn_readfirstlane(step_total);
+  // steps 0 .. n_full - 1 are the others, n_full .. n_steps - 1 upper-zero
+  const int n_full = __builtin_amdgcn_readfirstlane(step_total);
+  const int n_steps = n_full + __builtin_amdgcn_readfirstlane(step_hz);
+  auto entry = [&](int u) {
+    return __builtin_amdgcn_readfirstlane(
+        (int)steps[u < n_full ? u : 2 * kMaxTiles - 1 - (u - n_full)]);
+  };
 
   const uint16_t* qbase = p.q + head * p.qh;
   const uint16_t* dbase = p.dout + head * p.doh;
@@ -583,7 +614,7 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
   const float c = p.scale_log2;
 
   auto load_step = [&](int u, lds_u8* slot) {
-    const int t = __builtin_amdgcn_readfirstlane(steps[u]);
+    const int t = entry(u);
     const int64_t row0 = (int64_t)(t >> 1) * kTile + (t & 1) * kHalf;
     const char* qb = reinterpret_cast<const char*>(qbase + row0 * p.qs);
     const char* db = reinterpret_cast<const char*>(dbase + row0 * p.dos);
@@ -628,13 +659,16 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
       tro[db] = (16 * qb0 + rt) * 256 + (((2 * db + ((n >> 1) & 1)) ^ swzk(rt)) << 4) + 8 * (n & 1);
     const uint32_t roff = 4 * (16 * qb0 + 4 * g);  // the record's lse2 of the lane's rows
 
-    auto compute = [&](const lds_u8* slot) __attribute__((always_inline)) {
+    // NB (<= NQB) blocks of this wave's rows: NQB, or 2 (blocks 0, 1: rows
+    // 0 .. 31) in an upper-zero step of a wave of blocks 0 .. 3
+    auto compute = [&](auto nb, const lds_u8* slot) __attribute__((always_inline)) {
+      constexpr int NB = decltype(nb)::value;
       const lds_u8* qs = slot;
       const lds_u8* ds = slot + kHalfBytes;
       const lds_u8* rec = slot + kSlot;
-      f32x4 s[NQB], dp[NQB], lse[NQB];
+      f32x4 s[NB], dp[NB], lse[NB];
 #pragma unroll
-      for (int i = 0; i < NQB; ++i) {
+      for (int i = 0; i < NB; ++i) {
         s[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         dp[i] = *reinterpret_cast<const lds_f32x4*>(rec + 256 + roff + 64 * i);  // -D
         lse[i] = *reinterpret_cast<const lds_f32x4*>(rec + roff + 64 * i);
@@ -642,25 +676,25 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
-        for (int i = 0; i < NQB; ++i)
+        for (int i = 0; i < NB; ++i)
           s[i] = mfma16(lds16(qs + i * 4096 + arow[cc]), kf[cc], s[i]);
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
-        for (int i = 0; i < NQB; ++i)
+        for (int i = 0; i < NB; ++i)
           dp[i] = mfma16(lds16(ds + i * 4096 + arow[cc]), vf[cc], dp[i]);
       // issue order: the record reads, then each row read four products
       // ahead of its product
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * NQB + 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * NB + 4, 0);
 #pragma unroll
-      for (int x = 0; x < 8 * NQB - 4; ++x) {
+      for (int x = 0; x < 8 * NB - 4; ++x) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      uint32_t pp[NQB][2], pd[NQB][2];
+      uint32_t pp[NB][2], pd[NB][2];
 #pragma unroll
-      for (int i = 0; i < NQB; ++i) {
+      for (int i = 0; i < NB; ++i) {
         const f32x4 l4 = lse[i];
         float pr[4], dv[4];
 #pragma unroll
@@ -675,11 +709,11 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
         pd[i][0] = pack_bf16x2(dv[0], dv[1]);
         pd[i][1] = pack_bf16x2(dv[2], dv[3]);
       }
-      constexpr int NC = NQB == 1 ? 1 : NQB / 2;  // 32-row chunks
+      constexpr int NC = NB == 1 ? 1 : NB / 2;  // 32-row chunks
 #pragma unroll
       for (int qc = 0; qc < NC; ++qc) {
         u32x4 bp, bd;
-        if constexpr (NQB == 1) {
+        if constexpr (NB == 1) {
           bp = u32x4{pp[0][0], pp[0][1], 0u, 0u};
           bd = u32x4{pd[0][0], pd[0][1], 0u, 0u};
         } else {
@@ -692,18 +726,18 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
           const lds_u8* da = ds + qc * 8192 + tro[db];
           const lds_u8* qa = qs + qc * 8192 + tro[db];
           const u32x2 dlo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)da));
-          const u32x2 dhi = NQB == 1 ? zero2
+          const u32x2 dhi = NB == 1 ? zero2
                                      : __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                                                                      (lds_i16x4*)(da + 4096)));
           acc_v[db] = mfma16(u32x4{dlo[0], dlo[1], dhi[0], dhi[1]}, bp, acc_v[db]);
           const u32x2 qlo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)qa));
-          const u32x2 qhi = NQB == 1 ? zero2
+          const u32x2 qhi = NB == 1 ? zero2
                                      : __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                                                                      (lds_i16x4*)(qa + 4096)));
           acc_k[db] = mfma16(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, bd, acc_k[db]);
         }
         // issue order: the reads of head-dim block db + 1 before the products of db
-        constexpr int R = NQB == 1 ? 2 : 4;
+        constexpr int R = NB == 1 ? 2 : 4;
         __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
 #pragma unroll
         for (int db = 1; db < 8; ++db) {
@@ -716,19 +750,33 @@ __global__ void __launch_bounds__(kDkvThreads) __attribute__((amdgpu_waves_per_e
     // Step u: wait for this wave's loads (the only ones in flight), barrier
     // (every wave's loads of step u are in LDS and every wave is done reading
     // the other slot), issue step u + 1 into the other slot, compute step u.
-    auto run = [&](int u, lds_u8* cur, lds_u8* nxt) __attribute__((always_inline)) {
+    // The others first, then the upper-zero steps (hz), each walk with its
+    // own code, so the accumulators stay in one set of registers.
+    auto run = [&](auto hz, int u, lds_u8* cur, lds_u8* nxt) __attribute__((always_inline)) {
       VEDA_WAIT_VM(0);
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       if (u + 1 < n_steps) load_step(u + 1, nxt);
-      if (live) compute(cur);
+      if (live) {
+        if constexpr (!decltype(hz)::value)
+          compute(std::integral_constant<int, NQB>{}, cur);
+        else if constexpr (NQB == 4)
+          compute(std::integral_constant<int, 2>{}, cur);
+        else if (qb0 < 2)  // a wave of rows 32 .. 63 has nothing to add
+          compute(std::integral_constant<int, NQB>{}, cur);
+      }
+    };
+    auto walk = [&](auto hz, int u, int end) __attribute__((always_inline)) {
+      if (u < end && (u & 1)) run(hz, u++, s1, s0);
+      for (; u < end; u += 2) {
+        run(hz, u, s0, s1);
+        if (u + 1 >= end) break;
+        run(hz, u + 1, s1, s0);
+      }
     };
     if (n_steps > 0) load_step(0, s0);
-    for (int u = 0; u < n_steps; u += 2) {
-      run(u, s0, s1);
-      if (u + 1 >= n_steps) break;
-      run(u + 1, s1, s0);
-    }
+    walk(std::false_type{}, 0, n_full);
+    walk(std::true_type{}, n_full, n_steps);
     if constexpr (NQB < 4) {
       // the waves of key group kgrp (kgrp + NKG x part) hand their partial
       // sums to wave kgrp through the ring (free now); dV first, then dK
