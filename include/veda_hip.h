@@ -391,7 +391,10 @@ int veda_compensated_attention(const void* q, int64_t q_stride_s, int64_t q_stri
  * tiles, row stride list_ld); full_*_t / part_*_t: the transposed lists
  * (rows = key tiles, entries = query tiles, row stride list_ld_t), as
  * fa4.py:275-296 index_lists(transpose=True) builds them. Every row of
- * dq, dk, dv is written (0 where no block reaches it). workspace: at least
+ * dq, dk, dv is written (0 where no block reaches it). Rows whose dout is
+ * zero (+-0) and whose D is 0 add exactly zero for finite inputs, so 64-row
+ * halves (and 32-row groups) made of them are skipped: a layer's gradient
+ * through the scatter is zero on padding rows. workspace: at least
  * n_heads * n_q_tiles * 2048 bytes of device memory, 16-byte aligned
  * (per-row statistics; contents on entry do not matter).
  */
