@@ -273,12 +273,17 @@ def suite(reps: int = 5) -> dict:
                                                       return_lse=True)
     dout = torch.randn(o_f.shape, generator=torch.Generator(device='cuda').manual_seed(3),
                        device='cuda').to(torch.bfloat16)
-    ms_b = _median_ms(lambda: ops.block_sparse_bwd(c['qt'], c['kt'], c['vt'], o_f, dout, lse_f, None,
-                                                   *c['lists'], *lists_t, lay.valid_count,
-                                                   lay.n_tiles - lay.n_video_tiles), reps)
-    res['sparse_bwd_c2'] = _mfma(ms_b, 10.0 * 128 * 128 * D * kept)
-    res['sparse_bwd_c2']['vs_sparse_fwd'] = round(ms_b / ms, 3)
-    del lists_t, o_f, lse_f, dout
+    # the layer's gradient (zero on padding rows, whose outputs the scatter
+    # drops), then N(0, 1) on every row
+    dout_layer = dout * lay.slot_valid.to(dout.dtype)[:, None, None]
+    for key, d in (('sparse_bwd_c2', dout_layer), ('sparse_bwd_c2_every_row', dout)):
+        ms_b = _median_ms(lambda: ops.block_sparse_bwd(c['qt'], c['kt'], c['vt'], o_f, d, lse_f,
+                                                       None, *c['lists'], *lists_t,
+                                                       lay.valid_count,
+                                                       lay.n_tiles - lay.n_video_tiles), reps)
+        res[key] = _mfma(ms_b, 10.0 * 128 * 128 * D * kept)
+        res[key]['vs_sparse_fwd'] = round(ms_b / ms, 3)
+    del lists_t, o_f, lse_f, dout, dout_layer
     # zero-order compensation of the dropped tiles (summaries + the virtual-key
     # pass; the reference's Triton form costs 1.14x its sparse kernel)
     o_kept, lse_kept = kernels.block_sparse_attention_lists(c['qt'], c['kt'], c['vt'], c['lists'],
