@@ -972,6 +972,30 @@ __device__ __forceinline__ void vstep_fixed(const lds_u8* slot, const HFrag& fa,
 #undef VEDA_FENCE
 }
 
+// One sub-block (fragments f, first key k0) of virtual keys with the same
+// probability x for every positive weight: den += x * weight and O^T +=
+// V^T P^T, keys in the order vstep_fixed takes them.
+__device__ __forceinline__ void vsub_const(const lds_u8* slot, const HFrag& f, const uint8_t* wt,
+                                           int k0, int hi, float x, WaveState& w) {
+  u32x4 pk[2];
+  float den = 0.f;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t w4 = *reinterpret_cast<const uint32_t*>(wt + k0 + 8 * g + 4 * hi);
+    float ps[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const float ww = (float)((w4 >> (8 * m)) & 0xffu);
+      ps[m] = ww > 0.f ? x : 0.f;
+      den = fmaf(ps[m], ww, den);
+    }
+    pk[g >> 1][2 * (g & 1)] = pack_bf16x2(ps[0], ps[1]);
+    pk[g >> 1][2 * (g & 1) + 1] = pack_bf16x2(ps[2], ps[3]);
+  }
+  w.l_run += den;
+  sub_pv(slot, f, pk, w);
+}
+
 // vstep_fixed for a wave whose 32 query rows are all zero: every virtual
 // key scores exactly 0, so p = exp2(-ref2) (x0, per row) wherever the
 // key's weight is positive; only the P.V products remain. Same products,
@@ -980,27 +1004,45 @@ __device__ __forceinline__ void vstep_fixed(const lds_u8* slot, const HFrag& fa,
 __device__ __forceinline__ void vstep_fixed_zero(const lds_u8* slot, const HFrag& fa,
                                                  const HFrag& fb, const uint8_t* wt, int key0,
                                                  int hi, float x0, WaveState& w) {
-  auto sub = [&](const HFrag& f, int k0) {
-    u32x4 pk[2];
-    float den = 0.f;
+  vsub_const(slot, fa, wt, key0, hi, x0, w);
+  vsub_const(slot, fb, wt, key0 + 32, hi, x0, w);
+}
+
+// vstep_fixed over one sub-block (fragments f, first key k0) for a narrow
+// walk: its 8 score products, probabilities (den in vstep_fixed's key
+// order) and 8 P.V products.
+__device__ __forceinline__ void vstep_fixed_half(const lds_u8* slot, const HFrag& f, float c,
+                                                 const uint8_t* wt, int k0, int hi, float ref2,
+                                                 WaveState& w) {
+  typedef const __attribute__((address_space(3))) u32x4* lds_u32x4;
+  f32x16 s;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const uint32_t w4 = *reinterpret_cast<const uint32_t*>(wt + k0 + 8 * g + 4 * hi);
-      float ps[4];
+  for (int e = 0; e < 16; ++e) s[e] = 0.f;
+  u32x4 kf[8];
+  kf[0] = *reinterpret_cast<lds_u32x4>(slot + f.k[0]);
+  kf[1] = *reinterpret_cast<lds_u32x4>(slot + f.k[1]);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const float ww = (float)((w4 >> (8 * m)) & 0xffu);
-        ps[m] = ww > 0.f ? x0 : 0.f;
-        den = fmaf(ps[m], ww, den);
-      }
-      pk[g >> 1][2 * (g & 1)] = pack_bf16x2(ps[0], ps[1]);
-      pk[g >> 1][2 * (g & 1) + 1] = pack_bf16x2(ps[2], ps[3]);
+  for (int k = 0; k < 8; ++k) {
+    if (k + 2 < 8) kf[k + 2] = *reinterpret_cast<lds_u32x4>(slot + f.k[k + 2]);
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[k]), w.qf[k], s, 0, 0, 0);
+  }
+  u32x4 pk[2];
+  float den = 0.f;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t w4 = *reinterpret_cast<const uint32_t*>(wt + k0 + 8 * g + 4 * hi);
+    float ps[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const float ww = (float)((w4 >> (8 * m)) & 0xffu);
+      ps[m] = ww > 0.f ? __builtin_amdgcn_exp2f(fmaf(s[4 * g + m], c, -ref2)) : 0.f;
+      den = fmaf(ps[m], ww, den);
     }
-    w.l_run += den;
-    sub_pv(slot, f, pk, w);
-  };
-  sub(fa, key0);
-  sub(fb, key0 + 32);
+    pk[g >> 1][2 * (g & 1)] = pack_bf16x2(ps[0], ps[1]);
+    pk[g >> 1][2 * (g & 1) + 1] = pack_bf16x2(ps[2], ps[3]);
+  }
+  w.l_run += den;
+  sub_pv(slot, f, pk, w);
 }
 
 // One step of 64 virtual keys inside the online softmax (compensated
@@ -1368,11 +1410,11 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
       any |= x[0] | x[1] | x[2] | x[3];
     }
     q_zero = __ballot(any != 0) == 0;
-    if (MODE == kSparse && lane == 0) zflag[wave] = q_zero ? 1 : 0;
+    if ((MODE == kSparse || MODE == kVirtualOnly) && lane == 0) zflag[wave] = q_zero ? 1 : 0;
     // wave 0's Q fragments for wave 1 of a narrow walk (below), in ring
     // slot 1 past the step-list scratch; no load reaches slot 1 before the
     // walk's first barrier
-    if (MODE == kSparse && wave == 0) {
+    if ((MODE == kSparse || MODE == kVirtualOnly) && wave == 0) {
 #pragma unroll
       for (int s = 0; s < 8; ++s)
         *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
@@ -1429,6 +1471,28 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
   }
   const int n_small = LISTS ? __builtin_amdgcn_readfirstlane(step_small) : 0;
   const int n_steps = n_lsteps + n_virt;
+  // Narrow compensation (a tile whose only real rows are wave 0's): waves 0
+  // and 1 take wave 0's rows over sub-blocks a and b (wave 1 with wave 0's
+  // Q fragments and references); waves 2 and 3 sum, over sub-blocks a and
+  // b, the dropped tiles' V sums and weights that every all-zero row scales
+  // by its own exp2(-ref2). Merged after the walk.
+  bool vnarrow = false;
+  float ref2_w = ref2;  // the reference of the rows this wave walks
+  if (MODE == kVirtualOnly) {
+    const uint32_t zbits = __builtin_amdgcn_readfirstlane(
+        (uint32_t)zflag[0] | ((uint32_t)zflag[1] << 1) | ((uint32_t)zflag[2] << 2) |
+        ((uint32_t)zflag[3] << 3));
+    vnarrow = zbits == 0xEu && n_virt > 0;
+    if (vnarrow && wave == 1) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        w.qf[s] = as_bf16x8(*reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+            (const lds_u8*)ring[1] + kNarrowQ + (s * 64 + lane) * 16));
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // before slot 1 is loaded
+      const float lk0 = p.lse_kept[head * p.lk_h + (r * kTile + li) * p.lk_s];
+      ref2_w = lk0 > -INFINITY && lk0 < INFINITY ? lk0 * 1.4426950408889634f : 0.f;
+    }
+  }
 
   // Step u of the virtual and dense walks (the list walk decodes its own
   // steps): sub-block a is key rows row0 .. + 31 with la valid keys, sub-block
@@ -1897,8 +1961,14 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
     auto vwalk = [&](auto zero) __attribute__((always_inline)) {
       const float x0 = __builtin_amdgcn_exp2f(-ref2);
       auto vstep = [&](int v, const lds_u8* cur) __attribute__((always_inline)) {
-        if constexpr (decltype(zero)::value)
+        constexpr int K = decltype(zero)::value;
+        const int k0 = v * kHalf + 32 * (wave & 1);  // a narrow walk's sub-block
+        if constexpr (K == 1)
           vstep_fixed_zero(cur, fa, fb, vwt, v * kHalf, hi, x0, w);
+        else if constexpr (K == 2)
+          vstep_fixed_half(cur, fh, c, vwt, k0, hi, ref2_w, w);
+        else if constexpr (K == 3)
+          vsub_const(cur, fh, vwt, k0, hi, 1.f, w);
         else
           virtual_step(v, cur);
       };
@@ -1914,12 +1984,66 @@ __global__ void __launch_bounds__(kThreads2, 2) sfwd_kernel(FwdParams p) {
         vstep(u, s0);
       }
     };
-    if (MODE == kVirtualOnly && q_zero)
-      vwalk(std::true_type{});
+    if (MODE == kVirtualOnly && vnarrow)
+      wave < 2 ? vwalk(std::integral_constant<int, 2>{}) : vwalk(std::integral_constant<int, 3>{});
+    else if (MODE == kVirtualOnly && q_zero)
+      vwalk(std::integral_constant<int, 1>{});
     else
-      vwalk(std::false_type{});
+      vwalk(std::integral_constant<int, 0>{});
   }
   }  // the dense walk and the compensation of a given output
+
+  if (MODE == kVirtualOnly && vnarrow) {
+    // Merge the narrow compensation: wave 1's sums (wave 0's rows over
+    // sub-block b, against the same fixed references) into wave 0's; wave 3's
+    // V sum and weights (all columns alike; lanes 0 and 32 pass them) into
+    // wave 2's, which then hands the totals S and W to waves 1 to 3: an
+    // all-zero row with p = x0 = exp2(-ref2) on every positive weight has
+    // O = bf16(x0) S and den = x0 W. Through the last step's slot once every
+    // wave is done with it (the other slot holds the o_kept rows).
+    float* xo = reinterpret_cast<float*>(ring[(n_steps - 1) & 1]);
+    float* xz = xo + 65 * 64;
+    float* xs = xz + 132;
+    __syncthreads();
+    if (wave == 1) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xo[(16 * dt + e) * 64 + lane] = w.o[dt][e];
+      xo[64 * 64 + lane] = w.l_run;
+    } else if (wave == 3 && li == 0) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xz[(16 * dt + e) * 2 + hi] = w.o[dt][e];
+      xz[128 + hi] = w.l_run;
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) w.o[dt][e] += xo[(16 * dt + e) * 64 + lane];
+      w.l_run += xo[64 * 64 + lane];
+    } else if (wave == 2 && li == 0) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          xs[(16 * dt + e) * 2 + hi] = w.o[dt][e] + xz[(16 * dt + e) * 2 + hi];
+      xs[128 + hi] = w.l_run + xz[128 + hi];
+    }
+    __syncthreads();
+    if (wave != 0) {
+      const float x0 = __builtin_amdgcn_exp2f(-ref2);
+      const float xb = bf16_to_f32(pack_bf16x2(x0, 0.f) & 0xffffu);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) w.o[dt][e] = xb * xs[(16 * dt + e) * 2 + hi];
+      w.l_run = x0 * xs[128 + hi];
+    }
+  }
 
   if (MODE == kSparse && narrow) {
     // Merge the narrow walk's halves: wave 1's state (the real rows over

@@ -76,6 +76,36 @@ def test_compensation_matches_oracle():
     _bar(both, want32)
 
 
+def test_narrow_tiles_and_zero_rows_match_oracle():
+    """Query tiles whose only non-zero rows are their first 32 take the
+    narrow compensation (waves 0 and 1 split the real rows' virtual keys,
+    waves 2 and 3 sum the dropped tiles' V sums and weights, which every
+    all-zero row scales by its own exp2(-lse_kept)); other all-zero
+    groups take the product-free step. Here rows 32..127 of three full
+    tiles are zero (one of them keeps nothing), a 24-row tile too, and
+    every all-zero row gets its own o_kept and lse_kept, so the per-row
+    scaling is checked. Every row against the oracle on bf16 summaries."""
+    lay, olay, qt, kt, vt, mask = _case(2)
+    full = [int(t) for t in torch.nonzero(olay.valid_count == 128).flatten()[:4]]
+    qt = qt.clone()
+    for t in full[:3]:
+        qt[t * 128 + 32:(t + 1) * 128] = 0
+    qt[full[3] * 128 + 24:(full[3] + 1) * 128] = 0
+    mask[:, full[2]] = False
+    g = torch.Generator().manual_seed(5)
+    o = torch.randn(qt.shape, generator=g).to(torch.bfloat16)
+    lse = torch.randn(qt.shape[1], qt.shape[0], generator=g) * 2 + 3
+    lse[0, full[0] * 128 + 40] = float('-inf')  # a zero row that kept nothing
+    got = kernels.zero_order_compensation(o.cuda(), lse.cuda(), qt.cuda(), kt.cuda(), vt.cuda(),
+                                          mask.cuda(), lay).cpu()
+    want16 = oa.zero_order_compensation(o, lse, qt, kt, vt, mask, olay.valid_count,
+                                        torch.bfloat16)
+    torch.testing.assert_close(got.float(), want16.float(), rtol=1e-2, atol=4e-3)
+    rows = torch.cat([torch.arange(t * 128, (t + 1) * 128) for t in full])
+    torch.testing.assert_close(got.float()[rows], want16.float()[rows], rtol=1e-2, atol=4e-3)
+    assert (got.float()[rows] - o.float()[rows]).abs().max() > 5e-2
+
+
 def test_exact_when_dropped_tiles_hold_one_key():
     lay, olay, qt, kt, vt, mask = _case(1)
     n = olay.n_tiles
