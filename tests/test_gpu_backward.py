@@ -24,8 +24,9 @@ from tests import helpers
 pytestmark = pytest.mark.gpu
 
 
-def _ref_case(seed=0, ratio=0.3):
-    spec = helpers.small_layout()  # grid (8, 12, 20), 4x8x4 tiles: partial tiles
+def _ref_case(seed=0, ratio=0.3, spec=None):
+    if spec is None:
+        spec = helpers.small_layout()  # grid (8, 12, 20), 4x8x4 tiles: partial tiles
     lay = helpers.product_layout(*spec, device='cuda')
     olay = helpers.oracle_layout(*spec)
     q, k, v = helpers.qkv(lay.seq_len, 4, 128, seed=seed)
@@ -115,7 +116,8 @@ def test_lse_gradient():
         _bar(t.grad, w, name)
 
 
-def test_zero_gradient_rows_are_skipped_exactly():
+@pytest.mark.parametrize('layout', ['small', 'ragged'])
+def test_zero_gradient_rows_are_skipped_exactly(layout):
     """A layer's gradient through the scatter is zero on padding rows. A
     64-row half whose rows all have dO = 0 and D = 0 adds exactly zero to
     dK and dV (the dK/dV walk drops its step), and a dQ wave whose 32 rows
@@ -123,8 +125,12 @@ def test_zero_gradient_rows_are_skipped_exactly():
     padding row, on the second half of one full query tile and on a whole
     32-row group of another, and on the second half of a third tile where
     one row has a non-zero LSE gradient (D != 0: that half must still
-    count). Every gradient against the oracle."""
-    lay, olay, qt, kt, vt, mask, grad_out = _ref_case(4, ratio=0.5)
+    count). Every gradient against the oracle. The ragged layout adds key
+    tiles of at most 32 and at most 64 valid keys (the dK/dV kernel's
+    one- and two-block forms, whose waves of rows 32 .. 63 skip an
+    upper-zero step) and query tiles of 16 and 32 rows."""
+    spec = helpers.small_layout(grid=(5, 12, 20), shape='2x8x8') if layout == 'ragged' else None
+    lay, olay, qt, kt, vt, mask, grad_out = _ref_case(4, ratio=0.5, spec=spec)
     real = olay.slot_valid.bool().cuda()
     dout = grad_out * real.to(grad_out.dtype)[:, None, None]
     full = [int(t) for t in torch.nonzero(olay.valid_count == 128).flatten()[:3]]
